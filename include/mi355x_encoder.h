@@ -1,0 +1,150 @@
+/*
+ * mi355x_encoder.h -- C ABI of libmi355x_encoder.so, the gfx950 (MI355X)
+ * implementation of the Transformer encoder forward benchmarked by
+ * transformer_benchmark/models.py in the reference repository.
+ *
+ * Conventions shared by every entry point:
+ *   - All tensors are raw device pointers owned by the caller.  The library
+ *     never allocates or frees device memory and never synchronises the host,
+ *     so every call is safe inside HIP graph capture.
+ *   - bf16 tensors are passed as `void*` to 16-bit storage (IEEE bfloat16).
+ *     Activations are dense row-major; weights use nn.Linear's [out, in]
+ *     row-major layout, exactly as they sit in a PyTorch state_dict.
+ *   - `stream` is a hipStream_t (pass torch.cuda.current_stream().cuda_stream);
+ *     0 means the null stream.
+ *   - Return value 0 is success.  Any other value is an error code below and
+ *     enc_last_error() returns a message for the calling thread.  An
+ *     out-of-memory condition reported by HIP yields ENC_ERR_OOM and a message
+ *     containing "out of memory", so the reference runner's OOM classification
+ *     (runner.py:502-503) still applies.
+ *   - Masks are uint8 arrays (one byte per token, nonzero = valid token), the
+ *     byte view of a torch.bool [batch, seq_len] tensor.
+ */
+#ifndef MI355X_ENCODER_H
+#define MI355X_ENCODER_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ENC_OK 0
+#define ENC_ERR_INVALID 1     /* bad argument: null pointer, bad size     */
+#define ENC_ERR_UNSUPPORTED 2 /* shape outside what the kernels support   */
+#define ENC_ERR_HIP 3         /* a HIP runtime call or launch failed      */
+#define ENC_ERR_OOM 4         /* HIP reported out of memory               */
+
+/* Epilogues of enc_linear_bf16.  y = bf16(a . weight^T + bias) always comes
+ * first (fp32 accumulation, one rounding to bf16, the nn.Linear boundary). */
+#define ENC_EPI_BIAS 0               /* out = y                                   */
+#define ENC_EPI_BIAS_GELU 1          /* out = bf16(gelu_erf(y))                   */
+#define ENC_EPI_BIAS_RESIDUAL_KEEP 2 /* out = bf16(residual + y); masked rows:
+                                        out = residual                            */
+#define ENC_EPI_BIAS_RESIDUAL_ZERO 3 /* out = bf16(residual + y); masked rows:
+                                        out = 0                                   */
+
+/* Library version, (major << 16) | minor. */
+int enc_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* enc_last_error(void);
+
+/* LayerNorm over the last dimension with fp32 statistics:
+ *   y[r, :] = bf16(gamma * ((x[r, :] - mean) * rsqrt(var + eps)) + beta)
+ * If row_mask is non-null, rows with row_mask[r] == 0 are written as zeros
+ * (the masked_fill that follows final_norm).  width % 64 == 0, width <= 4096.
+ * Replaces nn.LayerNorm at transformer_benchmark/models.py:721,723,907 and the
+ * case-6 kernel wrapper transformer_benchmark/case6_exact_layer_norm.py:98-121
+ * (kernel host function case6_exact_layer_norm.cu:157-198). */
+int enc_layernorm_bf16(const void* x, const void* gamma, const void* beta,
+                       void* y, int64_t rows, int64_t width, float eps,
+                       const uint8_t* row_mask, void* stream);
+
+/* out[rows, out_features] = epilogue(a[rows, in_features] . weight^T + bias)
+ * with bf16 MFMA and fp32 accumulation.  residual (same shape as out) is read
+ * by the RESIDUAL epilogues only; row_mask (nullable, length rows) selects the
+ * masked-row behaviour described at the ENC_EPI_* constants.
+ * in_features % 64 == 0 and out_features % 64 == 0; rows is arbitrary.
+ * Replaces nn.Linear + F.gelu + residual add at transformer_benchmark/models.py:
+ * 76, 733-734 and the fused wrappers fused_ffn.py:91-126 (bias+GELU),
+ * fused_ffn_out.py:89-132 (bias+residual), fused_attention_out.py:89-130
+ * (out-proj+residual) and cublaslt_linear.py:292-344 (bias GEMM). */
+int enc_linear_bf16(const void* a, const void* weight, const void* bias,
+                    const void* residual, void* out, int64_t rows,
+                    int64_t out_features, int64_t in_features, int32_t epilogue,
+                    const uint8_t* row_mask, void* stream);
+
+/* Packed QKV projection x[batch*seq_len, d_model] . qkv_weight[3*d_model,
+ * d_model]^T + qkv_bias, rounded to bf16 and written head-major:
+ *   q, k : [batch, num_heads, seq_len, head_dim]
+ *   v_t  : [batch, num_heads, head_dim, seq_len]   (V transposed per head)
+ * head_dim = d_model / num_heads.  Replaces the packed projection and
+ * .contiguous() head split of transformer_benchmark/models.py:160-240 and the
+ * direct-layout wrapper direct_qkv.py:110-187 (baseline: models.py:35-53). */
+int enc_qkv_proj_bf16(const void* x, const void* weight, const void* bias,
+                      void* q, void* k, void* v_t, int64_t batch,
+                      int64_t seq_len, int64_t d_model, int64_t num_heads,
+                      void* stream);
+
+/* Streaming (online-softmax) attention; scores are never materialised.
+ * For each (b, h, query i), over keys j that are allowed:
+ *   s_ij = bf16(bf16(q_i . k_j) * scale)
+ *   p_ij = softmax_j(s_ij) in fp32 ;  context = bf16(sum_j bf16(p_ij) v_j)
+ * Key j is excluded when causal and j > i, when kv_len is non-null and
+ * j >= kv_len[b] (prefix padding), or when key_mask is non-null and
+ * key_mask[b, j] == 0.  With kv_len, query rows i >= kv_len[b] are padding and
+ * are written as zeros.  A query row with no allowed key is written as zeros.
+ * context: [batch, seq_len, num_heads * head_dim] (token-major, the layout
+ * out_proj consumes).  head_dim == 64.
+ * Replaces transformer_benchmark/models.py:55-75 (baseline) and the
+ * candidate's score/softmax/PV kernels: triangular_scores.py:110-291,
+ * pv_context.py:79-542, native_softmax_bf16.py:129-184,
+ * case6_exact_attention.py:119-148, case13_exact_attention.py:50-77. */
+int enc_attention_fwd_bf16(const void* q, const void* k, const void* v_t,
+                           void* context, int64_t batch, int64_t num_heads,
+                           int64_t seq_len, int64_t head_dim, float scale,
+                           int32_t causal, const int32_t* kv_len,
+                           const uint8_t* key_mask, void* stream);
+
+/* kv_len[b] = number of valid tokens in mask[b, :] (int32, device).  Equal to
+ * the prefix length for the prefix masks built by generate_random_case
+ * (transformer_benchmark/cases.py:87-97). */
+int enc_mask_lengths(const uint8_t* mask, int64_t batch, int64_t seq_len,
+                     int32_t* kv_len, void* stream);
+
+/* Bytes of device workspace enc_encoder_forward_bf16 needs for this shape. */
+int64_t enc_encoder_workspace_bytes(int64_t batch, int64_t seq_len,
+                                    int64_t d_model, int64_t num_heads,
+                                    int64_t ffn_dim);
+
+/* The whole encoder forward (num_layers blocks, then final LayerNorm):
+ *   per block  x = x + attention(norm1(x)) ; x = x + ffn_out(gelu(ffn_in(norm2(x))))
+ * weights: 12 * num_layers + 2 device pointers, per layer in the order
+ *   norm1.weight, norm1.bias, qkv_proj.weight [3D,D], qkv_proj.bias [3D],
+ *   out_proj.weight, out_proj.bias, norm2.weight, norm2.bias,
+ *   ffn_in.weight [F,D], ffn_in.bias, ffn_out.weight [D,F], ffn_out.bias,
+ * followed by final_norm.weight, final_norm.bias.
+ * Masking follows the reference: with row_mask non-null, padded rows of the
+ * attention output are zero (models.py:78-79), block outputs are zeroed on
+ * padded rows (models.py:736-737) and so is the final output
+ * (models.py:917-918).  kv_len / key_mask are passed to the attention as in
+ * enc_attention_fwd_bf16 (at most one of them non-null).  x is not modified;
+ * out may not alias x or the workspace.
+ * Replaces UserOptimizedTransformer.forward / _forward_eager
+ * (transformer_benchmark/models.py:1020-1049, 1202-1239) and the block
+ * forward (models.py:772-892). */
+int enc_encoder_forward_bf16(const void* x, void* out, void* workspace,
+                             int64_t workspace_bytes,
+                             const void* const* weights, int64_t batch,
+                             int64_t seq_len, int64_t d_model,
+                             int64_t num_heads, int64_t ffn_dim,
+                             int64_t num_layers, float eps, int32_t causal,
+                             const int32_t* kv_len, const uint8_t* key_mask,
+                             const uint8_t* row_mask, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MI355X_ENCODER_H */

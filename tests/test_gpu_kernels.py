@@ -1,0 +1,234 @@
+"""Kernel-level parity of libmi355x_encoder.so on the GPU.
+
+Each HIP kernel is called through the C ABI (via the ctypes binding) and checked
+against a plain PyTorch fp32 computation of the same op with the reference's
+bf16 rounding points, or against the oracle's attention restatement.
+"""
+
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle.encoder_oracle import attention_rows
+from tiktoktechjam2026track3_amd import native
+
+pytestmark = pytest.mark.gpu
+
+RTOL = 1.6e-2  # the build's bf16 gate
+ATOL = 1e-2
+
+
+def within_ulps(ref: torch.Tensor, out: torch.Tensor, ulps: float = 1.0) -> bool:
+    """|out - ref| <= ulps * bf16 spacing at |ref|, plus a floor of 2^-12 of the
+    tensor's rms for values near zero, where fp32 accumulation order alone moves
+    a cancelled result by many of its own (tiny) ulps."""
+    ref = ref.float()
+    out = out.float()
+    _, exponent = torch.frexp(ref)
+    spacing = torch.ldexp(torch.ones_like(ref), exponent - 8)  # bf16: 8 significant bits
+    floor = 2.0**-12 * ref.pow(2).mean().sqrt()
+    return bool(((out - ref).abs() <= ulps * spacing + floor).all())
+
+
+def bitwise_fraction(a: torch.Tensor, b: torch.Tensor) -> float:
+    return float((a.contiguous().view(torch.int16) == b.contiguous().view(torch.int16)).float().mean())
+
+
+def strict_gate(ref: torch.Tensor, out: torch.Tensor, rtol=RTOL, atol=ATOL) -> int:
+    ref = ref.float()
+    out = out.float()
+    err = (out - ref).abs()
+    ok = torch.isfinite(ref) & torch.isfinite(out) & ((err < atol) | (err < rtol * ref.abs()))
+    return int((~ok).sum().item())
+
+
+@pytest.fixture(autouse=True)
+def _no_tf32():
+    prev = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False
+    yield
+    torch.backends.cuda.matmul.allow_tf32 = prev
+
+
+def test_library_loads_and_reports_version():
+    lib = native.load_library()
+    assert lib.enc_version() >> 16 == 1
+
+
+@pytest.mark.parametrize("width", [256, 512, 1024])
+@pytest.mark.parametrize("rows", [1, 7, 4099])
+def test_layernorm_matches_torch(device, rows, width):
+    g = torch.Generator(device=device).manual_seed(rows * 7 + width)
+    x = (torch.randn(rows, width, generator=g, device=device) * 3 + 0.5).bfloat16()
+    w = (torch.randn(width, generator=g, device=device) * 0.5 + 1).bfloat16()
+    b = (torch.randn(width, generator=g, device=device) * 0.1).bfloat16()
+    ref = F.layer_norm(x.float(), (width,), w.float(), b.float(), 1e-5).bfloat16()
+    out = native.layernorm(x, w, b, 1e-5)
+    assert within_ulps(ref, out, 1)
+    # torch's own bf16 LayerNorm on the device (the reference's op): same
+    # rounding on all but a few elements in 10^4 (fp32 statistics order differs)
+    torch_bf16 = F.layer_norm(x, (width,), w, b, 1e-5)
+    assert strict_gate(torch_bf16, out) == 0
+    assert bitwise_fraction(torch_bf16, out) > 0.999
+
+
+def test_layernorm_row_mask_zeroes_rows(device):
+    x = torch.randn(64, 512, device=device).bfloat16()
+    w = torch.ones(512, device=device).bfloat16()
+    b = torch.full((512,), 0.25, device=device).bfloat16()
+    mask = torch.rand(64, device=device) > 0.5
+    out = native.layernorm(x, w, b, 1e-5, row_mask=mask)
+    assert torch.all(out[~mask] == 0)
+    ref = F.layer_norm(x.float(), (512,), w.float(), b.float(), 1e-5).bfloat16()
+    assert within_ulps(ref[mask], out[mask], 1)
+
+
+def _linear_case(device, m, n, k, seed):
+    g = torch.Generator(device=device).manual_seed(seed)
+    a = torch.randn(m, k, generator=g, device=device).bfloat16()
+    w = (torch.rand(n, k, generator=g, device=device) * 2 - 1).mul(1 / math.sqrt(k)).bfloat16()
+    bias = (torch.rand(n, generator=g, device=device) * 2 - 1).mul(1 / math.sqrt(k)).bfloat16()
+    res = torch.randn(m, n, generator=g, device=device).bfloat16()
+    y = F.linear(a.float(), w.float(), bias.float())  # fp32 reference
+    return a, w, bias, res, y
+
+
+SHAPES = [
+    (1, 512, 512),
+    (100, 1536, 512),
+    (128, 2048, 512),
+    (128, 512, 2048),
+    (1000, 1024, 1024),
+    (8192, 3072, 1024),
+    (8192, 1024, 4096),
+    (4096, 4096, 1024),
+]
+
+
+@pytest.mark.parametrize("m,n,k", SHAPES)
+def test_linear_bias(device, m, n, k):
+    a, w, bias, _, y = _linear_case(device, m, n, k, m + n + k)
+    out = native.linear(a, w, bias, native.ENC_EPI_BIAS)
+    assert within_ulps(y, out, 1)
+    # torch's bf16 nn.Linear (the reference op) accumulates in the same MFMA
+    # K order: the outputs agree bit for bit except where it splits K
+    assert bitwise_fraction(F.linear(a, w, bias), out) > 0.999
+
+
+@pytest.mark.parametrize("m,n,k", SHAPES[:6])
+def test_linear_gelu(device, m, n, k):
+    a, w, bias, _, y = _linear_case(device, m, n, k, 3 * m + n)
+    out = native.linear(a, w, bias, native.ENC_EPI_BIAS_GELU)
+    ref = F.gelu(y.bfloat16().float(), approximate="none").bfloat16()
+    assert strict_gate(ref, out) == 0
+    assert within_ulps(ref, out, 2)
+    assert bitwise_fraction(F.gelu(F.linear(a, w, bias), approximate="none"), out) > 0.999
+
+
+@pytest.mark.parametrize("epi", [native.ENC_EPI_BIAS_RESIDUAL_KEEP, native.ENC_EPI_BIAS_RESIDUAL_ZERO])
+@pytest.mark.parametrize("m,n,k", [(100, 512, 512), (8192, 1024, 1024), (1000, 1024, 4096)])
+def test_linear_residual(device, m, n, k, epi):
+    a, w, bias, res, y = _linear_case(device, m, n, k, 5 * m + k)
+    mask = torch.rand(m, device=device) > 0.3
+    out = native.linear(a, w, bias, epi, residual=res, row_mask=mask)
+    ref = (res.float() + y.bfloat16().float()).bfloat16()
+    assert strict_gate(ref[mask], out[mask]) == 0
+    assert within_ulps(ref[mask], out[mask], 2)
+    torch_ref = res + F.linear(a, w, bias)
+    assert bitwise_fraction(torch_ref[mask], out[mask]) > 0.999
+    if epi == native.ENC_EPI_BIAS_RESIDUAL_KEEP:
+        assert torch.equal(out[~mask], res[~mask])
+    else:
+        assert torch.all(out[~mask] == 0)
+    # no mask: every row takes the residual sum
+    out2 = native.linear(a, w, bias, epi, residual=res)
+    assert within_ulps(ref, out2, 2)
+
+
+@pytest.mark.parametrize("b,s,d,h", [(1, 128, 512, 8), (2, 100, 512, 8), (8, 1024, 1024, 16), (3, 37, 1024, 16)])
+def test_qkv_head_major(device, b, s, d, h):
+    g = torch.Generator(device=device).manual_seed(b * s + d)
+    x = torch.randn(b, s, d, generator=g, device=device).bfloat16()
+    w = (torch.randn(3 * d, d, generator=g, device=device) / math.sqrt(d)).bfloat16()
+    bias = (torch.randn(3 * d, generator=g, device=device) * 0.05).bfloat16()
+    q, k, v_t = native.qkv_proj(x, w, bias, h)
+    y = F.linear(x.float(), w.float(), bias.float()).bfloat16()
+    hd = d // h
+    ref = y.view(b, s, 3, h, hd).permute(2, 0, 3, 1, 4)  # [3, B, H, S, hd]
+    assert within_ulps(ref[0], q, 1) and within_ulps(ref[1], k, 1)
+    assert within_ulps(ref[2].transpose(-1, -2), v_t[..., :s], 1)
+    packed = F.linear(x, w, bias).view(b, s, 3, h, hd).permute(2, 0, 3, 1, 4)
+    assert bitwise_fraction(packed[0], q) > 0.999 and bitwise_fraction(packed[1], k) > 0.999
+
+
+def _attention_inputs(device, b, h, s, seed):
+    g = torch.Generator(device=device).manual_seed(seed)
+    q = torch.randn(b, h, s, 64, generator=g, device=device).bfloat16()
+    k = torch.randn(b, h, s, 64, generator=g, device=device).bfloat16()
+    v = torch.randn(b, h, s, 64, generator=g, device=device).bfloat16()
+    ld = native.vt_stride(s)
+    v_t = torch.full((b, h, 64, ld), float("nan"), device=device, dtype=torch.bfloat16)
+    v_t[..., :s] = v.transpose(-1, -2)
+    return q, k, v, v_t
+
+
+def _oracle_context(q, k, v, causal, mask):
+    b, h, s, hd = q.shape
+    ctx = attention_rows(q, k, v, hd**-0.5, causal, mask, torch.arange(s, device=q.device))
+    return ctx.transpose(1, 2).reshape(b, s, h * hd)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("b,h,s", [(1, 1, 1), (1, 2, 63), (2, 3, 64), (1, 2, 100), (2, 8, 128), (1, 4, 1000), (2, 16, 1024)])
+def test_attention_unmasked(device, b, h, s, causal):
+    q, k, v, v_t = _attention_inputs(device, b, h, s, 11 * s + b)
+    out = native.attention(q, k, v_t, 0.125, causal)
+    ref = _oracle_context(q, k, v, causal, None)
+    assert strict_gate(ref, out) == 0, f"max abs {float((ref.float() - out.float()).abs().max())}"
+    # exact two-pass softmax: the same bf16 probabilities as the reference up to
+    # rare last-bit differences of exp/sum order
+    assert bitwise_fraction(ref, out) > 0.99
+    if causal:
+        # row 0 attends only to key 0: its context is v[:, :, 0] exactly
+        assert torch.equal(out[:, 0, :].view(b, h, 64), v[:, :, 0, :])
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("b,h,s", [(4, 2, 256), (3, 4, 1000), (2, 2, 8192)])
+def test_attention_prefix_padding(device, b, h, s, causal):
+    q, k, v, v_t = _attention_inputs(device, b, h, s, 13 * s + b)
+    g = torch.Generator(device=device).manual_seed(s)
+    lengths = torch.randint(max(1, s // 2), s + 1, (b,), generator=g, device=device)
+    lengths[0] = 1 if b > 1 else lengths[0]
+    mask = torch.arange(s, device=device)[None, :] < lengths[:, None]
+    kv_len = native.mask_lengths(mask)
+    assert torch.equal(kv_len.long(), lengths)
+    out = native.attention(q, k, v_t, 0.125, causal, kv_len=kv_len)
+    ref = _oracle_context(q, k, v, causal, mask)
+    valid = mask[..., None].expand_as(out)
+    assert strict_gate(ref[valid], out[valid]) == 0
+    assert torch.all(out[~valid] == 0)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_attention_general_mask(device, causal):
+    b, h, s = 2, 4, 300
+    q, k, v, v_t = _attention_inputs(device, b, h, s, 99)
+    g = torch.Generator(device=device).manual_seed(5)
+    mask = torch.rand(b, s, generator=g, device=device) > 0.4
+    mask[:, 0] = True
+    out = native.attention(q, k, v_t, 0.125, causal, key_mask=mask)
+    ref = _oracle_context(q, k, v, causal, mask)
+    rows = mask[..., None].expand_as(out)  # valid query rows always see >= 1 key
+    assert strict_gate(ref[rows], out[rows]) == 0
+
+
+def test_attention_non_power_of_two_scale(device):
+    q, k, v, v_t = _attention_inputs(device, 1, 2, 200, 7)
+    scale = 0.1
+    out = native.attention(q, k, v_t, scale, False)
+    ctx = attention_rows(q, k, v, scale, False, None, torch.arange(200, device=device))
+    ref = ctx.transpose(1, 2).reshape(1, 200, 128)
+    assert strict_gate(ref, out) == 0

@@ -1,0 +1,93 @@
+"""Build libmi355x_encoder.so (gfx950) in-tree with hipcc.
+
+Usage: ``python -m tiktoktechjam2026track3_amd.build_native`` or
+``build_native.build()``.  Each ``csrc/*.hip`` file is compiled to an object in
+``csrc/_build/`` in parallel, then linked into ``libmi355x_encoder.so`` next to
+this file.  The library is always rebuilt when ``build()`` is called.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PACKAGE_DIR = Path(__file__).resolve().parent
+CSRC_DIR = PACKAGE_DIR / "csrc"
+BUILD_DIR = CSRC_DIR / "_build"
+LIBRARY_NAME = "libmi355x_encoder.so"
+LIBRARY_PATH = PACKAGE_DIR / LIBRARY_NAME
+OFFLOAD_ARCH = "gfx950"
+
+SOURCES = ("layernorm.hip", "gemm.hip", "attention.hip", "capi.hip")
+
+# Packed FP32 VALU ops (v_pk_fma_f32 and friends) are disabled for every device
+# compile; hipcc's host pass prints a harmless "not a recognized feature" note.
+COMMON_FLAGS = (
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    f"--offload-arch={OFFLOAD_ARCH}",
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+    "-Wall",
+    "-Wno-unused-function",
+    "-Wno-unused-command-line-argument",
+)
+
+
+def _hipcc() -> str:
+    candidate = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(candidate).exists():
+        raise RuntimeError("hipcc not found; the gfx950 HIP library cannot be built")
+    return candidate
+
+
+def _run(cmd: list[str]) -> None:
+    proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    noise = "is not a recognized feature for this target"
+    output = "\n".join(
+        line for line in proc.stdout.splitlines() if noise not in line
+    ).strip()
+    if proc.returncode != 0:
+        raise RuntimeError(f"command failed ({proc.returncode}): {' '.join(cmd)}\n{output}")
+    if output:
+        print(output, file=sys.stderr)
+
+
+def build(verbose: bool = False, jobs: int | None = None) -> Path:
+    """Compile every HIP source for gfx950 and link the shared library."""
+    hipcc = _hipcc()
+    BUILD_DIR.mkdir(parents=True, exist_ok=True)
+    include = f"-I{PACKAGE_DIR.parent / 'include'}"
+    objects = []
+    commands = []
+    for name in SOURCES:
+        src = CSRC_DIR / name
+        obj = BUILD_DIR / (src.stem + ".o")
+        objects.append(obj)
+        commands.append([hipcc, *COMMON_FLAGS, include, "-c", str(src), "-o", str(obj)])
+    workers = jobs or min(len(commands), max(1, (os.cpu_count() or 2)))
+    if verbose:
+        for cmd in commands:
+            print(" ".join(cmd))
+    with ThreadPoolExecutor(max_workers=workers) as pool:
+        for future in [pool.submit(_run, cmd) for cmd in commands]:
+            future.result()
+    tmp = LIBRARY_PATH.with_suffix(".so.tmp")
+    link = [hipcc, "-shared", "-fPIC", f"--offload-arch={OFFLOAD_ARCH}", *map(str, objects), "-o", str(tmp)]
+    if verbose:
+        print(" ".join(link))
+    _run(link)
+    os.replace(tmp, LIBRARY_PATH)
+    return LIBRARY_PATH
+
+
+if __name__ == "__main__":
+    path = build(verbose="-v" in sys.argv)
+    print(path)

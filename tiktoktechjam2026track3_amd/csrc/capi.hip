@@ -1,0 +1,310 @@
+// extern "C" boundary of libmi355x_encoder.so (declared in include/mi355x_encoder.h).
+//
+// Every entry point validates its arguments, launches on the caller's stream and
+// returns a status code; the message of the last failure is kept per thread.
+// Nothing here allocates device memory or synchronises the host.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/mi355x_encoder.h"
+#include "common.h"
+#include "kernels.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+
+int fail_hip(hipError_t err, const char* where) {
+  std::string msg = std::string(where) + ": " + hipGetErrorString(err);
+  if (err == hipErrorOutOfMemory || err == hipErrorMemoryAllocation) {
+    return fail(ENC_ERR_OOM, msg + " (out of memory)");
+  }
+  return fail(ENC_ERR_HIP, msg);
+}
+
+int ok() {
+  g_last_error.clear();
+  return ENC_OK;
+}
+
+// Compute units of the current device, cached per device ordinal.
+int device_cus() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
+    cache[dev] = cus;
+  }
+  return cache[dev];
+}
+
+inline int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
+
+// Workspace carve-up for the encoder forward.
+struct EncoderWorkspace {
+  int64_t ln, q, k, vt, ctx, xa, xb, hidden, total;
+};
+
+EncoderWorkspace plan_workspace(int64_t B, int64_t S, int64_t D, int64_t H, int64_t F) {
+  const int64_t T = B * S;
+  const int64_t hd = D / H;
+  const int64_t e = 2;  // bf16 bytes
+  EncoderWorkspace w{};
+  int64_t off = 0;
+  auto take = [&](int64_t bytes) {
+    const int64_t at = off;
+    off = align_up(off + bytes, 256);
+    return at;
+  };
+  w.ln = take(T * D * e);
+  w.q = take(T * D * e);
+  w.k = take(T * D * e);
+  w.vt = take(B * H * hd * enc::vt_stride(S) * e);
+  w.ctx = take(T * D * e);
+  w.xa = take(T * D * e);
+  w.xb = take(T * D * e);
+  w.hidden = take(T * F * e);
+  w.total = off;
+  return w;
+}
+
+bool shape_ok(int64_t v) { return v > 0 && v < (int64_t(1) << 31); }
+
+int check_encoder_shape(int64_t B, int64_t S, int64_t D, int64_t H, int64_t F) {
+  if (!shape_ok(B) || !shape_ok(S) || !shape_ok(D) || !shape_ok(H) || !shape_ok(F))
+    return fail(ENC_ERR_INVALID, "batch, seq_len, d_model, num_heads and ffn_dim must be positive");
+  if (D % H != 0) return fail(ENC_ERR_INVALID, "d_model must be divisible by num_heads");
+  if (D / H != 64)
+    return fail(ENC_ERR_UNSUPPORTED, "attention kernel supports head_dim == 64 only (got " +
+                                         std::to_string(D / H) + ")");
+  if (!enc::layernorm_supported(D))
+    return fail(ENC_ERR_UNSUPPORTED, "LayerNorm width must be a power of two in [64, 4096] (got " +
+                                         std::to_string(D) + ")");
+  if (D % 64 != 0 || F % 64 != 0)
+    return fail(ENC_ERR_UNSUPPORTED, "d_model and ffn_dim must be multiples of 64");
+  if (B * S >= (int64_t(1) << 31)) return fail(ENC_ERR_UNSUPPORTED, "batch * seq_len must be < 2^31");
+  return ENC_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int enc_version(void) { return (1 << 16) | 0; }
+
+const char* enc_last_error(void) { return g_last_error.c_str(); }
+
+int enc_layernorm_bf16(const void* x, const void* gamma, const void* beta, void* y, int64_t rows,
+                       int64_t width, float eps, const uint8_t* row_mask, void* stream) {
+  if (rows < 0 || width <= 0) return fail(ENC_ERR_INVALID, "layernorm: rows must be >= 0 and width > 0");
+  if (rows == 0) return ok();
+  if (!x || !gamma || !beta || !y) return fail(ENC_ERR_INVALID, "layernorm: null tensor pointer");
+  if (!enc::layernorm_supported(width))
+    return fail(ENC_ERR_UNSUPPORTED, "layernorm: width must be a power of two in [64, 4096]");
+  if (!(eps > 0.f)) return fail(ENC_ERR_INVALID, "layernorm: eps must be positive");
+  hipError_t e = enc::layernorm_bf16(static_cast<const enc::bf16_t*>(x), static_cast<const enc::bf16_t*>(gamma),
+                                     static_cast<const enc::bf16_t*>(beta), static_cast<enc::bf16_t*>(y), rows,
+                                     width, eps, row_mask, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail_hip(e, "layernorm launch");
+  return ok();
+}
+
+int enc_linear_bf16(const void* a, const void* weight, const void* bias, const void* residual,
+                    void* out, int64_t rows, int64_t out_features, int64_t in_features,
+                    int32_t epilogue, const uint8_t* row_mask, void* stream) {
+  if (epilogue < ENC_EPI_BIAS || epilogue > ENC_EPI_BIAS_RESIDUAL_ZERO)
+    return fail(ENC_ERR_INVALID, "linear: unknown epilogue " + std::to_string(epilogue));
+  if (rows < 0 || out_features <= 0 || in_features <= 0)
+    return fail(ENC_ERR_INVALID, "linear: rows must be >= 0, features > 0");
+  if (rows == 0) return ok();
+  if (!a || !weight || !bias || !out) return fail(ENC_ERR_INVALID, "linear: null tensor pointer");
+  const bool needs_res = epilogue == ENC_EPI_BIAS_RESIDUAL_KEEP || epilogue == ENC_EPI_BIAS_RESIDUAL_ZERO;
+  if (needs_res && !residual) return fail(ENC_ERR_INVALID, "linear: residual epilogue needs a residual");
+  if (!enc::gemm_supported(rows, out_features, in_features))
+    return fail(ENC_ERR_UNSUPPORTED, "linear: in_features and out_features must be multiples of 64 (got " +
+                                         std::to_string(in_features) + ", " + std::to_string(out_features) + ")");
+  enc::GemmEpilogueArgs ep;
+  ep.bias = static_cast<const enc::bf16_t*>(bias);
+  ep.residual = static_cast<const enc::bf16_t*>(residual);
+  ep.row_mask = row_mask;
+  ep.out = static_cast<enc::bf16_t*>(out);
+  hipError_t e = enc::gemm_bf16(static_cast<const enc::bf16_t*>(a), static_cast<const enc::bf16_t*>(weight), rows,
+                                out_features, in_features, epilogue, ep, device_cus(),
+                                static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail_hip(e, "linear launch");
+  return ok();
+}
+
+int enc_qkv_proj_bf16(const void* x, const void* weight, const void* bias, void* q, void* k, void* v_t,
+                      int64_t batch, int64_t seq_len, int64_t d_model, int64_t num_heads, void* stream) {
+  if (batch < 0 || seq_len < 0 || d_model <= 0 || num_heads <= 0)
+    return fail(ENC_ERR_INVALID, "qkv: bad shape");
+  if (batch == 0 || seq_len == 0) return ok();
+  if (!x || !weight || !bias || !q || !k || !v_t) return fail(ENC_ERR_INVALID, "qkv: null tensor pointer");
+  if (d_model % num_heads != 0) return fail(ENC_ERR_INVALID, "qkv: d_model must be divisible by num_heads");
+  const int64_t M = batch * seq_len;
+  if (!enc::gemm_supported(M, 3 * d_model, d_model))
+    return fail(ENC_ERR_UNSUPPORTED, "qkv: d_model must be a multiple of 64");
+  enc::GemmEpilogueArgs ep;
+  ep.bias = static_cast<const enc::bf16_t*>(bias);
+  ep.q = static_cast<enc::bf16_t*>(q);
+  ep.k = static_cast<enc::bf16_t*>(k);
+  ep.v_t = static_cast<enc::bf16_t*>(v_t);
+  ep.seq_len = static_cast<int>(seq_len);
+  ep.num_heads = static_cast<int>(num_heads);
+  ep.head_dim = static_cast<int>(d_model / num_heads);
+  ep.d_model = static_cast<int>(d_model);
+  ep.ld_vt = static_cast<int>(enc::vt_stride(seq_len));
+  hipError_t e = enc::gemm_bf16(static_cast<const enc::bf16_t*>(x), static_cast<const enc::bf16_t*>(weight), M,
+                                3 * d_model, d_model, enc::kEpiQkvHeadMajor, ep, device_cus(),
+                                static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail_hip(e, "qkv launch");
+  return ok();
+}
+
+int enc_attention_fwd_bf16(const void* q, const void* k, const void* v_t, void* context, int64_t batch,
+                           int64_t num_heads, int64_t seq_len, int64_t head_dim, float scale, int32_t causal,
+                           const int32_t* kv_len, const uint8_t* key_mask, void* stream) {
+  if (batch < 0 || num_heads <= 0 || seq_len < 0 || head_dim <= 0)
+    return fail(ENC_ERR_INVALID, "attention: bad shape");
+  if (batch == 0 || seq_len == 0) return ok();
+  if (!q || !k || !v_t || !context) return fail(ENC_ERR_INVALID, "attention: null tensor pointer");
+  if (head_dim != 64) return fail(ENC_ERR_UNSUPPORTED, "attention: head_dim must be 64");
+  if (kv_len && key_mask) return fail(ENC_ERR_INVALID, "attention: pass kv_len or key_mask, not both");
+  if (!(scale > 0.f)) return fail(ENC_ERR_INVALID, "attention: scale must be positive");
+  if (batch * num_heads * ((seq_len + 127) / 128) >= (int64_t(1) << 31))
+    return fail(ENC_ERR_UNSUPPORTED, "attention: grid too large");
+  hipError_t e = enc::attention_fwd_bf16(
+      static_cast<const enc::bf16_t*>(q), static_cast<const enc::bf16_t*>(k), static_cast<const enc::bf16_t*>(v_t),
+      static_cast<enc::bf16_t*>(context), static_cast<int>(batch), static_cast<int>(num_heads),
+      static_cast<int>(seq_len), static_cast<int>(head_dim), scale, causal != 0, kv_len, key_mask,
+      static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail_hip(e, "attention launch");
+  return ok();
+}
+
+int enc_mask_lengths(const uint8_t* mask, int64_t batch, int64_t seq_len, int32_t* kv_len, void* stream) {
+  if (batch < 0 || seq_len < 0) return fail(ENC_ERR_INVALID, "mask_lengths: bad shape");
+  if (batch == 0) return ok();
+  if (!mask || !kv_len) return fail(ENC_ERR_INVALID, "mask_lengths: null pointer");
+  hipError_t e = enc::mask_lengths(mask, batch, seq_len, kv_len, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail_hip(e, "mask_lengths launch");
+  return ok();
+}
+
+int64_t enc_encoder_workspace_bytes(int64_t batch, int64_t seq_len, int64_t d_model, int64_t num_heads,
+                                    int64_t ffn_dim) {
+  if (!shape_ok(batch) || !shape_ok(seq_len) || !shape_ok(d_model) || !shape_ok(num_heads) || !shape_ok(ffn_dim) ||
+      d_model % num_heads != 0)
+    return -1;
+  return plan_workspace(batch, seq_len, d_model, num_heads, ffn_dim).total;
+}
+
+int enc_encoder_forward_bf16(const void* x, void* out, void* workspace, int64_t workspace_bytes,
+                             const void* const* weights, int64_t batch, int64_t seq_len, int64_t d_model,
+                             int64_t num_heads, int64_t ffn_dim, int64_t num_layers, float eps, int32_t causal,
+                             const int32_t* kv_len, const uint8_t* key_mask, const uint8_t* row_mask,
+                             void* stream) {
+  int rc = check_encoder_shape(batch, seq_len, d_model, num_heads, ffn_dim);
+  if (rc != ENC_OK) return rc;
+  if (num_layers < 0) return fail(ENC_ERR_INVALID, "encoder: num_layers must be >= 0");
+  if (!x || !out || !workspace || !weights) return fail(ENC_ERR_INVALID, "encoder: null pointer");
+  if (kv_len && key_mask) return fail(ENC_ERR_INVALID, "encoder: pass kv_len or key_mask, not both");
+  if (!(eps > 0.f)) return fail(ENC_ERR_INVALID, "encoder: eps must be positive");
+  const EncoderWorkspace w = plan_workspace(batch, seq_len, d_model, num_heads, ffn_dim);
+  if (workspace_bytes < w.total)
+    return fail(ENC_ERR_INVALID, "encoder: workspace too small (" + std::to_string(workspace_bytes) + " < " +
+                                     std::to_string(w.total) + ")");
+  for (int64_t i = 0; i < 12 * num_layers + 2; ++i)
+    if (!weights[i]) return fail(ENC_ERR_INVALID, "encoder: null weight pointer at index " + std::to_string(i));
+
+  using enc::bf16_t;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  char* base = static_cast<char*>(workspace);
+  bf16_t* ln = reinterpret_cast<bf16_t*>(base + w.ln);
+  bf16_t* q = reinterpret_cast<bf16_t*>(base + w.q);
+  bf16_t* k = reinterpret_cast<bf16_t*>(base + w.k);
+  bf16_t* vt = reinterpret_cast<bf16_t*>(base + w.vt);
+  bf16_t* ctx = reinterpret_cast<bf16_t*>(base + w.ctx);
+  bf16_t* xa = reinterpret_cast<bf16_t*>(base + w.xa);
+  bf16_t* xb = reinterpret_cast<bf16_t*>(base + w.xb);
+  bf16_t* hidden = reinterpret_cast<bf16_t*>(base + w.hidden);
+
+  const int64_t T = batch * seq_len;
+  const int64_t D = d_model, F = ffn_dim, H = num_heads;
+  const int cus = device_cus();
+  const float scale = 1.0f / sqrtf(static_cast<float>(D / H));
+  auto W = [&](int64_t layer, int idx) { return static_cast<const bf16_t*>(weights[layer * 12 + idx]); };
+
+  const bf16_t* cur = static_cast<const bf16_t*>(x);
+  hipError_t e = hipSuccess;
+  for (int64_t layer = 0; layer < num_layers; ++layer) {
+    bf16_t* x_attn = (cur == xa) ? xb : xa;  // residual stream after attention
+    // norm1
+    e = enc::layernorm_bf16(cur, W(layer, 0), W(layer, 1), ln, T, D, eps, nullptr, st);
+    if (e != hipSuccess) return fail_hip(e, "encoder norm1");
+    // packed QKV, head-major
+    enc::GemmEpilogueArgs qa;
+    qa.bias = W(layer, 3);
+    qa.q = q;
+    qa.k = k;
+    qa.v_t = vt;
+    qa.seq_len = static_cast<int>(seq_len);
+    qa.num_heads = static_cast<int>(H);
+    qa.head_dim = static_cast<int>(D / H);
+    qa.d_model = static_cast<int>(D);
+    qa.ld_vt = static_cast<int>(enc::vt_stride(seq_len));
+    e = enc::gemm_bf16(ln, W(layer, 2), T, 3 * D, D, enc::kEpiQkvHeadMajor, qa, cus, st);
+    if (e != hipSuccess) return fail_hip(e, "encoder qkv");
+    // attention -> context [T, D]
+    e = enc::attention_fwd_bf16(q, k, vt, ctx, static_cast<int>(batch), static_cast<int>(H),
+                                static_cast<int>(seq_len), static_cast<int>(D / H), scale, causal != 0, kv_len,
+                                key_mask, st);
+    if (e != hipSuccess) return fail_hip(e, "encoder attention");
+    // out_proj + residual; padded rows keep the residual (attention output is 0 there)
+    enc::GemmEpilogueArgs oa;
+    oa.bias = W(layer, 5);
+    oa.residual = cur;
+    oa.row_mask = row_mask;
+    oa.out = x_attn;
+    e = enc::gemm_bf16(ctx, W(layer, 4), T, D, D, enc::kEpiResidualKeep, oa, cus, st);
+    if (e != hipSuccess) return fail_hip(e, "encoder out_proj");
+    // norm2
+    e = enc::layernorm_bf16(x_attn, W(layer, 6), W(layer, 7), ln, T, D, eps, nullptr, st);
+    if (e != hipSuccess) return fail_hip(e, "encoder norm2");
+    // ffn_in + exact GELU
+    enc::GemmEpilogueArgs fa;
+    fa.bias = W(layer, 9);
+    fa.out = hidden;
+    e = enc::gemm_bf16(ln, W(layer, 8), T, F, D, enc::kEpiBiasGelu, fa, cus, st);
+    if (e != hipSuccess) return fail_hip(e, "encoder ffn_in");
+    // ffn_out + residual; padded rows are zeroed (block output masked_fill)
+    bf16_t* x_next = (x_attn == xa) ? xb : xa;
+    enc::GemmEpilogueArgs fo;
+    fo.bias = W(layer, 11);
+    fo.residual = x_attn;
+    fo.row_mask = row_mask;
+    fo.out = x_next;
+    e = enc::gemm_bf16(hidden, W(layer, 10), T, D, F, enc::kEpiResidualZero, fo, cus, st);
+    if (e != hipSuccess) return fail_hip(e, "encoder ffn_out");
+    cur = x_next;
+  }
+  e = enc::layernorm_bf16(cur, static_cast<const bf16_t*>(weights[12 * num_layers]),
+                          static_cast<const bf16_t*>(weights[12 * num_layers + 1]), static_cast<bf16_t*>(out), T, D,
+                          eps, row_mask, st);
+  if (e != hipSuccess) return fail_hip(e, "encoder final_norm");
+  return ok();
+}
+
+}  // extern "C"

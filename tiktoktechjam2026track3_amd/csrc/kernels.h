@@ -1,0 +1,62 @@
+// Internal launchers shared between the kernel files and the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "common.h"
+
+namespace enc {
+
+// Epilogue selectors of the GEMM kernel (values 0..3 mirror ENC_EPI_*).
+enum Epilogue : int {
+  kEpiBias = 0,
+  kEpiBiasGelu = 1,
+  kEpiResidualKeep = 2,
+  kEpiResidualZero = 3,
+  kEpiQkvHeadMajor = 4,
+};
+
+struct GemmEpilogueArgs {
+  const bf16_t* bias = nullptr;      // [N]
+  const bf16_t* residual = nullptr;  // [M, N]
+  const uint8_t* row_mask = nullptr; // [M] or null
+  bf16_t* out = nullptr;             // [M, N] row-major
+  // head-major QKV outputs (kEpiQkvHeadMajor only)
+  bf16_t* q = nullptr;   // [B, H, S, hd]
+  bf16_t* k = nullptr;   // [B, H, S, hd]
+  bf16_t* v_t = nullptr; // [B, H, hd, ld_vt]
+  int seq_len = 0;
+  int num_heads = 0;
+  int head_dim = 0;
+  int d_model = 0;
+  int ld_vt = 0;
+};
+
+// LayerNorm
+bool layernorm_supported(int64_t width);
+hipError_t layernorm_bf16(const bf16_t* x, const bf16_t* gamma, const bf16_t* beta, bf16_t* y,
+                          int64_t rows, int64_t width, float eps, const uint8_t* row_mask,
+                          hipStream_t stream);
+
+// GEMM: C[M, N] = A[M, K] . W[N, K]^T with the given epilogue.
+// Requirements: N % 64 == 0, K % 64 == 0, M >= 0.
+bool gemm_supported(int64_t M, int64_t N, int64_t K);
+hipError_t gemm_bf16(const bf16_t* A, const bf16_t* W, int64_t M, int64_t N, int64_t K,
+                     int epilogue, const GemmEpilogueArgs& ep, int num_cus, hipStream_t stream);
+
+// Tile shape the dispatcher picks for (M, N) on a device with num_cus CUs.
+void gemm_pick_tile(int64_t M, int64_t N, int epilogue, int num_cus, int* bm, int* bn);
+
+// Attention (head_dim 64).  v_t row stride is ld_vt = round_up(S, 8).
+hipError_t attention_fwd_bf16(const bf16_t* q, const bf16_t* k, const bf16_t* v_t, bf16_t* ctx,
+                              int batch, int heads, int seq_len, int head_dim, float scale,
+                              bool causal, const int32_t* kv_len, const uint8_t* key_mask,
+                              hipStream_t stream);
+
+hipError_t mask_lengths(const uint8_t* mask, int64_t batch, int64_t seq_len, int32_t* kv_len,
+                        hipStream_t stream);
+
+inline int64_t vt_stride(int64_t seq_len) { return (seq_len + 7) / 8 * 8; }
+
+}  // namespace enc

@@ -1,0 +1,608 @@
+"""Encoder models: the PyTorch baseline and the MI355X-native candidate.
+
+The plugin boundary is the reference's (transformer_benchmark/models.py):
+``BaselineTransformer(config)`` and ``UserOptimizedTransformer(config)``, both
+``forward(x, valid_token_mask=None) -> [B, S, D]``, with the baseline's parameter
+names so ``copy_model_weights`` (models.py:1242-1255) moves a baseline state_dict
+into the candidate, including the legacy q/k/v -> packed ``qkv_proj`` conversion
+(models.py:105-158).
+
+Baseline (models.py:17-80, 718-738, 895-919): the reference math with native
+torch ops, module construction order kept so ``torch.manual_seed(s)`` gives the
+same default-init weights.  When the full ``[B, H, S, S]`` score tensor would not
+fit a memory budget the same per-row math is evaluated over query-row blocks
+(softmax is row-local), which is what lets the S = 100000 shape run at all.
+
+Candidate: on CPU it runs the same op sequence as the baseline (the reference's
+CPU fallback contract, tests/test_models.py:30-67).  On a HIP device with bf16
+tensors the whole forward is one call into libmi355x_encoder.so
+(``enc_encoder_forward_bf16``); small shapes are captured once into a HIP graph
+and replayed (models.py:1051-1118, 1163-1239).  Any other dtype on the GPU, or a
+shape the kernels do not support, raises ``UnsupportedShapeError``; there is no
+silent fallback.
+"""
+
+from __future__ import annotations
+
+import copy
+import weakref
+from dataclasses import dataclass
+from typing import Dict, List, Optional, Tuple
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .cases import TransformerConfig
+
+# Upper bound on the bytes of score temporaries one baseline attention call may
+# hold at once; above it the baseline walks query-row blocks.
+SCORE_MEMORY_BUDGET_BYTES = 16 * 1024**3
+# Bytes per score element the baseline keeps alive at peak (bf16 scores, the
+# scaled/masked copies, fp32 softmax input and output, bf16 probabilities).
+SCORE_BYTES_PER_ELEMENT = 16
+
+# Token count up to which the candidate captures a HIP graph (launch-bound shapes).
+GRAPH_MAX_TOKENS = 4096
+
+
+class UnsupportedShapeError(NotImplementedError):
+    """The native kernels do not cover this shape/dtype; no fallback is taken."""
+
+
+def _attention_core(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    scale: float,
+    causal: bool,
+    valid_token_mask: Optional[torch.Tensor],
+    row_start: int,
+    row_stop: int,
+) -> torch.Tensor:
+    """Reference score/softmax/PV math for query rows [row_start, row_stop)."""
+    seq_len = k.shape[-2]
+    scores = torch.matmul(q[..., row_start:row_stop, :], k.transpose(-2, -1)) * scale
+    if causal:
+        rows = torch.arange(row_start, row_stop, device=q.device)[:, None]
+        cols = torch.arange(seq_len, device=q.device)[None, :]
+        scores = scores.masked_fill(cols > rows, float("-inf"))
+    if valid_token_mask is not None:
+        scores = scores.masked_fill(~valid_token_mask[:, None, None, :], float("-inf"))
+    probs = torch.softmax(scores.float(), dim=-1).to(dtype=q.dtype)
+    return torch.matmul(probs, v)
+
+
+class BaselineSelfAttention(nn.Module):
+    """Multi-head self-attention with native PyTorch ops (models.py:17-80)."""
+
+    def __init__(self, d_model: int, num_heads: int) -> None:
+        super().__init__()
+        if d_model % num_heads != 0:
+            raise ValueError("d_model must be divisible by num_heads")
+        self.d_model = d_model
+        self.num_heads = num_heads
+        self.head_dim = d_model // num_heads
+        self.scale = self.head_dim**-0.5
+        self.q_proj = nn.Linear(d_model, d_model, bias=True)
+        self.k_proj = nn.Linear(d_model, d_model, bias=True)
+        self.v_proj = nn.Linear(d_model, d_model, bias=True)
+        self.out_proj = nn.Linear(d_model, d_model, bias=True)
+
+    def _split_heads(self, x: torch.Tensor) -> torch.Tensor:
+        b, s, _ = x.shape
+        return x.view(b, s, self.num_heads, self.head_dim).transpose(1, 2).contiguous()
+
+    def _context(
+        self,
+        q: torch.Tensor,
+        k: torch.Tensor,
+        v: torch.Tensor,
+        valid_token_mask: Optional[torch.Tensor],
+        causal: bool,
+    ) -> torch.Tensor:
+        b, h, s, _ = q.shape
+        per_row = b * h * s * SCORE_BYTES_PER_ELEMENT
+        if per_row * s <= SCORE_MEMORY_BUDGET_BYTES:
+            return _attention_core(q, k, v, self.scale, causal, valid_token_mask, 0, s)
+        # Row-blocked evaluation of the identical per-row math.
+        block = max(1, SCORE_MEMORY_BUDGET_BYTES // per_row)
+        out = torch.empty_like(q)
+        for start in range(0, s, block):
+            stop = min(s, start + block)
+            out[..., start:stop, :] = _attention_core(
+                q, k, v, self.scale, causal, valid_token_mask, start, stop
+            )
+        return out
+
+    def forward(
+        self,
+        x: torch.Tensor,
+        valid_token_mask: Optional[torch.Tensor] = None,
+        causal: bool = False,
+    ) -> torch.Tensor:
+        b, s, _ = x.shape
+        q = self._split_heads(self.q_proj(x))
+        k = self._split_heads(self.k_proj(x))
+        v = self._split_heads(self.v_proj(x))
+        context = self._context(q, k, v, valid_token_mask, causal)
+        context = context.transpose(1, 2).contiguous().view(b, s, self.d_model)
+        output = self.out_proj(context)
+        if valid_token_mask is not None:
+            output = output.masked_fill(~valid_token_mask[..., None], 0)
+        return output
+
+
+class BaselineTransformerBlock(nn.Module):
+    """Pre-norm encoder block (models.py:718-738)."""
+
+    def __init__(self, d_model: int, num_heads: int, ffn_dim: int) -> None:
+        super().__init__()
+        self.norm1 = nn.LayerNorm(d_model)
+        self.attention = BaselineSelfAttention(d_model, num_heads)
+        self.norm2 = nn.LayerNorm(d_model)
+        self.ffn_in = nn.Linear(d_model, ffn_dim)
+        self.ffn_out = nn.Linear(ffn_dim, d_model)
+
+    def forward(
+        self,
+        x: torch.Tensor,
+        valid_token_mask: Optional[torch.Tensor],
+        causal: bool,
+    ) -> torch.Tensor:
+        x = x + self.attention(self.norm1(x), valid_token_mask, causal)
+        x = x + self.ffn_out(F.gelu(self.ffn_in(self.norm2(x)), approximate="none"))
+        if valid_token_mask is not None:
+            x = x.masked_fill(~valid_token_mask[..., None], 0)
+        return x
+
+
+class BaselineTransformer(nn.Module):
+    """L blocks then a final LayerNorm (models.py:895-919)."""
+
+    def __init__(self, config: TransformerConfig) -> None:
+        super().__init__()
+        self.config = config
+        self.layers = nn.ModuleList(
+            [
+                BaselineTransformerBlock(config.d_model, config.num_heads, config.ffn_dim)
+                for _ in range(config.num_layers)
+            ]
+        )
+        self.final_norm = nn.LayerNorm(config.d_model)
+
+    def forward(
+        self,
+        x: torch.Tensor,
+        valid_token_mask: Optional[torch.Tensor] = None,
+    ) -> torch.Tensor:
+        for layer in self.layers:
+            x = layer(x, valid_token_mask, self.config.causal)
+        x = self.final_norm(x)
+        if valid_token_mask is not None:
+            x = x.masked_fill(~valid_token_mask[..., None], 0)
+        return x
+
+
+# --------------------------------------------------------------------------
+# Candidate
+# --------------------------------------------------------------------------
+
+_LEGACY = ("q_proj", "k_proj", "v_proj")
+
+
+class UserOptimizedSelfAttention(BaselineSelfAttention):
+    """Packed [3D, D] Q/K/V projection plus out_proj (models.py:83-158)."""
+
+    def __init__(self, d_model: int, num_heads: int, seq_len: int) -> None:
+        nn.Module.__init__(self)
+        if d_model % num_heads != 0:
+            raise ValueError("d_model must be divisible by num_heads")
+        self.d_model = d_model
+        self.num_heads = num_heads
+        self.head_dim = d_model // num_heads
+        self.scale = self.head_dim**-0.5
+        self.seq_len = seq_len
+        self.qkv_proj = nn.Linear(d_model, 3 * d_model, bias=True)
+        self.out_proj = nn.Linear(d_model, d_model, bias=True)
+
+    def _load_from_state_dict(
+        self,
+        state_dict: Dict[str, torch.Tensor],
+        prefix: str,
+        local_metadata: Dict[str, object],
+        strict: bool,
+        missing_keys: List[str],
+        unexpected_keys: List[str],
+        error_msgs: List[str],
+    ) -> None:
+        legacy = [f"{prefix}{name}.{kind}" for kind in ("weight", "bias") for name in _LEGACY]
+        present = [key for key in legacy if key in state_dict]
+        packed_w, packed_b = f"{prefix}qkv_proj.weight", f"{prefix}qkv_proj.bias"
+        if present:
+            if len(present) != len(legacy):
+                missing = sorted(set(legacy) - set(present))
+                error_msgs.append(f"incomplete legacy Q/K/V state for {prefix}: missing {missing}")
+            elif packed_w in state_dict or packed_b in state_dict:
+                error_msgs.append(f"ambiguous packed and legacy Q/K/V state for {prefix}")
+            else:
+                for kind, packed in (("weight", packed_w), ("bias", packed_b)):
+                    parts = [state_dict.pop(f"{prefix}{name}.{kind}") for name in _LEGACY]
+                    state_dict[packed] = torch.cat(parts, dim=0)
+        super()._load_from_state_dict(
+            state_dict, prefix, local_metadata, strict, missing_keys, unexpected_keys, error_msgs
+        )
+
+    def forward(
+        self,
+        x: torch.Tensor,
+        valid_token_mask: Optional[torch.Tensor] = None,
+        causal: bool = False,
+        residual: Optional[torch.Tensor] = None,
+    ) -> torch.Tensor:
+        """Eager torch path (CPU): the baseline op sequence on packed weights.
+
+        The three projections are evaluated as separate [D, D] linears on views
+        of the packed weight so the arithmetic is call-for-call the baseline's.
+        """
+        b, s, d = x.shape
+        w, bias = self.qkv_proj.weight, self.qkv_proj.bias
+        q = self._split_heads(F.linear(x, w[:d], bias[:d]))
+        k = self._split_heads(F.linear(x, w[d : 2 * d], bias[d : 2 * d]))
+        v = self._split_heads(F.linear(x, w[2 * d :], bias[2 * d :]))
+        context = self._context(q, k, v, valid_token_mask, causal)
+        context = context.transpose(1, 2).contiguous().view(b, s, d)
+        output = self.out_proj(context)
+        if valid_token_mask is not None:
+            output = output.masked_fill(~valid_token_mask[..., None], 0)
+        if residual is not None:
+            output = residual + output
+        return output
+
+
+class UserOptimizedTransformerBlock(BaselineTransformerBlock):
+    def __init__(self, d_model: int, num_heads: int, ffn_dim: int, seq_len: int) -> None:
+        super().__init__(d_model, num_heads, ffn_dim)
+        self.attention = UserOptimizedSelfAttention(d_model, num_heads, seq_len)
+
+    def forward(
+        self,
+        x: torch.Tensor,
+        valid_token_mask: Optional[torch.Tensor],
+        causal: bool,
+    ) -> torch.Tensor:
+        x = self.attention(self.norm1(x), valid_token_mask, causal, residual=x)
+        x = x + self.ffn_out(F.gelu(self.ffn_in(self.norm2(x)), approximate="none"))
+        if valid_token_mask is not None:
+            x = x.masked_fill(~valid_token_mask[..., None], 0)
+        return x
+
+
+@dataclass(frozen=True)
+class _MaskMetadata:
+    object_id: int
+    device: torch.device
+    dtype: torch.dtype
+    shape: Tuple[int, ...]
+    strides: Tuple[int, ...]
+    storage_data_ptr: int
+    storage_offset: int
+    version: int
+
+
+@dataclass
+class _MaskCacheEntry:
+    reference: "weakref.ReferenceType[torch.Tensor]"
+    metadata: _MaskMetadata
+    kind: str  # "all_true" | "prefix" | "general"
+
+
+MASK_ALL_TRUE = "all_true"
+MASK_PREFIX = "prefix"
+MASK_GENERAL = "general"
+
+
+def classify_mask(mask: torch.Tensor) -> str:
+    """all_true, prefix (row b valid exactly on [0, len_b)) or general (one host sync)."""
+    if bool(mask.all().item()):
+        return MASK_ALL_TRUE
+    lengths = mask.sum(dim=1, keepdim=True)
+    positions = torch.arange(mask.shape[1], device=mask.device).unsqueeze(0)
+    return MASK_PREFIX if bool(torch.equal(positions < lengths, mask)) else MASK_GENERAL
+
+
+class _HipState:
+    """Per-model cached launch state of the native forward."""
+
+    def __init__(self) -> None:
+        self.weight_signature: Optional[Tuple[int, ...]] = None
+        self.weight_table: Optional[torch.Tensor] = None
+        self.eps: float = 1e-5
+        self.workspace: Optional[torch.Tensor] = None
+        self.workspace_key: Optional[Tuple[object, ...]] = None
+
+
+class UserOptimizedTransformer(BaselineTransformer):
+    """Drop-in candidate: same signature and parameter names as the baseline."""
+
+    def __init__(self, config: TransformerConfig) -> None:
+        nn.Module.__init__(self)
+        self.config = config
+        self.layers = nn.ModuleList(
+            [
+                UserOptimizedTransformerBlock(
+                    config.d_model, config.num_heads, config.ffn_dim, config.seq_len
+                )
+                for _ in range(config.num_layers)
+            ]
+        )
+        self.final_norm = nn.LayerNorm(config.d_model)
+        # Runtime-only state, deliberately not parameters or buffers so weight
+        # copying and serialisation match the baseline.
+        self._hip = _HipState()
+        self._cuda_graph: Optional[torch.cuda.CUDAGraph] = None
+        self._cuda_graph_output: Optional[torch.Tensor] = None
+        self._cuda_graph_stream: Optional[torch.cuda.Stream] = None
+        self._cuda_graph_signature: Optional[Tuple[object, ...]] = None
+        self._cuda_graph_capture_count = 0
+        self._mask_cache_entry: Optional[_MaskCacheEntry] = None
+
+    # ---- mask classification (cached per tensor version, models.py:1122-1161) ----
+
+    @staticmethod
+    def _mask_metadata(mask: torch.Tensor) -> Optional[_MaskMetadata]:
+        try:
+            version = mask._version
+        except RuntimeError:  # inference tensors outside inference mode
+            return None
+        return _MaskMetadata(
+            object_id=id(mask),
+            device=mask.device,
+            dtype=mask.dtype,
+            shape=tuple(mask.shape),
+            strides=tuple(mask.stride()),
+            storage_data_ptr=mask.untyped_storage().data_ptr(),
+            storage_offset=mask.storage_offset(),
+            version=version,
+        )
+
+    def _mask_kind(self, mask: torch.Tensor) -> str:
+        metadata = self._mask_metadata(mask)
+        if metadata is None:
+            self._mask_cache_entry = None
+            return classify_mask(mask)
+        entry = self._mask_cache_entry
+        if entry is not None and entry.reference() is mask and entry.metadata == metadata:
+            return entry.kind
+        kind = classify_mask(mask)
+        confirmed = self._mask_metadata(mask)
+        if confirmed != metadata or confirmed is None:
+            self._mask_cache_entry = None
+            return MASK_GENERAL
+        self._mask_cache_entry = _MaskCacheEntry(weakref.ref(mask), confirmed, kind)
+        return kind
+
+    def _mask_is_all_true(self, mask: torch.Tensor) -> bool:
+        return self._mask_kind(mask) == MASK_ALL_TRUE
+
+    # ---- CPU / eager torch path ----
+
+    def _forward_eager(
+        self,
+        x: torch.Tensor,
+        valid_token_mask: Optional[torch.Tensor],
+    ) -> torch.Tensor:
+        for layer in self.layers:
+            x = layer(x, valid_token_mask, self.config.causal)
+        x = self.final_norm(x)
+        if valid_token_mask is not None:
+            x = x.masked_fill(~valid_token_mask[..., None], 0)
+        return x
+
+    # ---- native path ----
+
+    def _check_native_supported(self, x: torch.Tensor) -> None:
+        cfg = self.config
+        if x.dtype != torch.bfloat16:
+            raise UnsupportedShapeError(
+                f"the MI355X kernels run bfloat16 only (got {x.dtype} on {x.device})"
+            )
+        if x.dim() != 3 or x.shape[-1] != cfg.d_model:
+            raise ValueError(f"expected x of shape [B, S, {cfg.d_model}], got {tuple(x.shape)}")
+        hd = cfg.d_model // cfg.num_heads
+        problems = []
+        if hd != 64:
+            problems.append(f"head_dim {hd} (supported: 64)")
+        if cfg.d_model not in (64, 128, 256, 512, 1024, 2048, 4096):
+            problems.append(f"d_model {cfg.d_model} (supported: powers of two 64..4096)")
+        if cfg.ffn_dim % 64 != 0:
+            problems.append(f"ffn_dim {cfg.ffn_dim} (must be a multiple of 64)")
+        if problems:
+            raise UnsupportedShapeError("unsupported encoder shape: " + ", ".join(problems))
+
+    def _native_weights(self, device: torch.device) -> Tuple[torch.Tensor, float]:
+        params: List[torch.Tensor] = []
+        eps_values = set()
+        for layer in self.layers:
+            attn = layer.attention
+            params += [
+                layer.norm1.weight, layer.norm1.bias,
+                attn.qkv_proj.weight, attn.qkv_proj.bias,
+                attn.out_proj.weight, attn.out_proj.bias,
+                layer.norm2.weight, layer.norm2.bias,
+                layer.ffn_in.weight, layer.ffn_in.bias,
+                layer.ffn_out.weight, layer.ffn_out.bias,
+            ]
+            eps_values.update((layer.norm1.eps, layer.norm2.eps))
+        params += [self.final_norm.weight, self.final_norm.bias]
+        eps_values.add(self.final_norm.eps)
+        if len(eps_values) != 1:
+            raise UnsupportedShapeError("all LayerNorms must share one eps")
+        for p in params:
+            if p.device != device or p.dtype != torch.bfloat16 or not p.is_contiguous():
+                raise UnsupportedShapeError(
+                    "parameters must be contiguous bfloat16 tensors on the input's device"
+                )
+        signature = tuple(p.data_ptr() for p in params)
+        state = self._hip
+        if state.weight_signature != signature:
+            state.weight_table = torch.tensor(signature, dtype=torch.int64)
+            state.weight_signature = signature
+            state.eps = float(next(iter(eps_values)))
+        assert state.weight_table is not None
+        return state.weight_table, state.eps
+
+    def _native_workspace(self, x: torch.Tensor) -> torch.Tensor:
+        from . import native
+
+        cfg = self.config
+        b, s, _ = x.shape
+        key = (x.device, b, s)
+        state = self._hip
+        if state.workspace is None or state.workspace_key != key:
+            state.workspace = None
+            size = native.encoder_workspace_bytes(b, s, cfg.d_model, cfg.num_heads, cfg.ffn_dim)
+            state.workspace = torch.empty(size, device=x.device, dtype=torch.uint8)
+            state.workspace_key = key
+        return state.workspace
+
+    def _forward_native(
+        self,
+        x: torch.Tensor,
+        valid_token_mask: Optional[torch.Tensor],
+        mask_kind: str,
+    ) -> torch.Tensor:
+        from . import native
+
+        cfg = self.config
+        self._check_native_supported(x)
+        x = x.contiguous()
+        table, eps = self._native_weights(x.device)
+        workspace = self._native_workspace(x)
+        out = torch.empty_like(x)
+        kv_len = key_mask = row_mask = None
+        if valid_token_mask is not None and mask_kind != MASK_ALL_TRUE:
+            mask = valid_token_mask.contiguous()
+            row_mask = mask.view(torch.uint8)
+            if mask_kind == MASK_PREFIX:
+                kv_len = native.mask_lengths(mask)
+            else:
+                key_mask = row_mask
+        native.encoder_forward(
+            x, out, workspace, table, cfg.num_heads, cfg.ffn_dim, cfg.num_layers, eps,
+            cfg.causal, kv_len, key_mask, row_mask,
+        )
+        return out
+
+    # ---- HIP graph replay for launch-bound shapes ----
+
+    def _cuda_graph_eligible(self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor]) -> bool:
+        cfg = self.config
+        if self.training or torch.is_grad_enabled():
+            return False
+        if x.device.type != "cuda" or x.dtype != torch.bfloat16 or not x.is_contiguous():
+            return False
+        if tuple(x.shape) != (cfg.batch_size, cfg.seq_len, cfg.d_model):
+            return False
+        if cfg.batch_size * cfg.seq_len > GRAPH_MAX_TOKENS:
+            return False
+        if valid_token_mask is not None and (
+            valid_token_mask.device != x.device
+            or valid_token_mask.dtype != torch.bool
+            or tuple(valid_token_mask.shape) != (cfg.batch_size, cfg.seq_len)
+            or not valid_token_mask.is_contiguous()
+        ):
+            return False
+        return True
+
+    def _cuda_graph_live_signature(
+        self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor], mask_kind: str
+    ) -> Tuple[object, ...]:
+        mask_part: Tuple[object, ...] = (None,)
+        if valid_token_mask is not None:
+            mask_part = (
+                valid_token_mask.untyped_storage().data_ptr(),
+                tuple(valid_token_mask.shape),
+                tuple(valid_token_mask.stride()),
+                valid_token_mask.storage_offset(),
+            )
+        return (
+            x.untyped_storage().data_ptr(),
+            tuple(x.shape),
+            tuple(x.stride()),
+            x.storage_offset(),
+            *mask_part,
+            mask_kind,
+            tuple(p.untyped_storage().data_ptr() for p in self.parameters()),
+        )
+
+    def _capture_cuda_graph(
+        self,
+        x: torch.Tensor,
+        valid_token_mask: Optional[torch.Tensor],
+        mask_kind: str,
+        signature: Tuple[object, ...],
+    ) -> torch.Tensor:
+        self._cuda_graph = None
+        self._cuda_graph_output = None
+        self._cuda_graph_stream = None
+        self._cuda_graph_signature = None
+
+        replay_stream = torch.cuda.current_stream(x.device)
+        capture_stream = torch.cuda.Stream(device=x.device)
+        capture_stream.wait_stream(replay_stream)
+        with torch.cuda.stream(capture_stream), torch.inference_mode():
+            for _ in range(2):
+                self._forward_native(x, valid_token_mask, mask_kind)
+        replay_stream.wait_stream(capture_stream)
+        torch.cuda.synchronize(x.device)
+
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=capture_stream):
+            graph_output = self._forward_native(x, valid_token_mask, mask_kind)
+
+        self._cuda_graph = graph
+        self._cuda_graph_output = graph_output
+        self._cuda_graph_stream = capture_stream
+        self._cuda_graph_signature = signature
+        self._cuda_graph_capture_count += 1
+        if self._cuda_graph_capture_count == 1:
+            print(f"[optimized] captured HIP graph for shape={tuple(x.shape)}")
+        graph.replay()
+        return graph_output.clone()
+
+    # ---- entry point ----
+
+    def forward(
+        self,
+        x: torch.Tensor,
+        valid_token_mask: Optional[torch.Tensor] = None,
+    ) -> torch.Tensor:
+        if not self._cuda_graph_eligible(x, valid_token_mask):
+            if x.device.type != "cuda":
+                return self._forward_eager(x, valid_token_mask)
+            mask_kind = MASK_ALL_TRUE
+            if valid_token_mask is not None:
+                mask_kind = self._mask_kind(valid_token_mask)
+            return self._forward_native(x, valid_token_mask, mask_kind)
+
+        mask_kind = MASK_ALL_TRUE
+        if valid_token_mask is not None:
+            mask_kind = self._mask_kind(valid_token_mask)
+        signature = self._cuda_graph_live_signature(x, valid_token_mask, mask_kind)
+        if self._cuda_graph_signature != signature:
+            return self._capture_cuda_graph(x, valid_token_mask, mask_kind, signature)
+        assert self._cuda_graph is not None and self._cuda_graph_output is not None
+        self._cuda_graph.replay()
+        return self._cuda_graph_output.clone()
+
+
+def copy_model_weights(baseline: nn.Module, optimized: nn.Module, strict: bool = True) -> None:
+    """Copy the baseline's weights into the candidate (models.py:1242-1255)."""
+    state_dict = copy.deepcopy(baseline.state_dict())
+    result = optimized.load_state_dict(state_dict, strict=strict)
+    if not strict:
+        if result.missing_keys:
+            print(f"[warning] missing optimized keys: {result.missing_keys}")
+        if result.unexpected_keys:
+            print(f"[warning] unexpected optimized keys: {result.unexpected_keys}")

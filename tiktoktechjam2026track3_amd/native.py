@@ -1,0 +1,308 @@
+"""ctypes binding of libmi355x_encoder.so (the C ABI in include/mi355x_encoder.h).
+
+The library is loaded once, under a lock, the way the reference loads its native
+extensions (transformer_benchmark/native_softmax_bf16.py:16-17, 129-136) and binds
+a C library through ctypes with explicit argtypes/restype and status codes mapped
+to Python exceptions (transformer_benchmark/cublaslt_linear.py:57-60, 71-144).
+
+There is no fallback: if the library is missing or fails to load, every call
+raises ``NativeLibraryError`` naming the path and the build command.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+from typing import Optional
+
+import torch
+
+LIBRARY_PATH = Path(__file__).resolve().parent / "libmi355x_encoder.so"
+HEADER_PATH = Path(__file__).resolve().parent.parent / "include" / "mi355x_encoder.h"
+
+ENC_OK = 0
+ENC_ERR_INVALID = 1
+ENC_ERR_UNSUPPORTED = 2
+ENC_ERR_HIP = 3
+ENC_ERR_OOM = 4
+
+ENC_EPI_BIAS = 0
+ENC_EPI_BIAS_GELU = 1
+ENC_EPI_BIAS_RESIDUAL_KEEP = 2
+ENC_EPI_BIAS_RESIDUAL_ZERO = 3
+
+# (name, restype, argtypes) for every exported symbol.
+_VP = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I32 = ctypes.c_int32
+_F32 = ctypes.c_float
+SIGNATURES = (
+    ("enc_version", ctypes.c_int, ()),
+    ("enc_last_error", ctypes.c_char_p, ()),
+    ("enc_layernorm_bf16", ctypes.c_int, (_VP, _VP, _VP, _VP, _I64, _I64, _F32, _VP, _VP)),
+    ("enc_linear_bf16", ctypes.c_int, (_VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I32, _VP, _VP)),
+    ("enc_qkv_proj_bf16", ctypes.c_int, (_VP, _VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _VP)),
+    (
+        "enc_attention_fwd_bf16",
+        ctypes.c_int,
+        (_VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _F32, _I32, _VP, _VP, _VP),
+    ),
+    ("enc_mask_lengths", ctypes.c_int, (_VP, _I64, _I64, _VP, _VP)),
+    ("enc_encoder_workspace_bytes", ctypes.c_int64, (_I64, _I64, _I64, _I64, _I64)),
+    (
+        "enc_encoder_forward_bf16",
+        ctypes.c_int,
+        (_VP, _VP, _VP, _I64, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _F32, _I32, _VP, _VP, _VP, _VP),
+    ),
+)
+
+
+class NativeLibraryError(RuntimeError):
+    """libmi355x_encoder.so is missing or failed to load."""
+
+
+class EncoderKernelError(RuntimeError):
+    """A C-ABI call returned a nonzero status."""
+
+    def __init__(self, name: str, code: int, message: str) -> None:
+        super().__init__(f"{name} failed with status {code}: {message}")
+        self.code = code
+
+
+_lock = threading.Lock()
+_lib: Optional[ctypes.CDLL] = None
+
+
+def load_library(path: Optional[Path] = None) -> ctypes.CDLL:
+    """Load and bind the shared library (once per process)."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    with _lock:
+        if _lib is not None and path is None:
+            return _lib
+        target = Path(path) if path is not None else LIBRARY_PATH
+        if not target.exists():
+            raise NativeLibraryError(
+                f"{target} not found; build it with "
+                "`python -m tiktoktechjam2026track3_amd.build_native`"
+            )
+        try:
+            lib = ctypes.CDLL(str(target))
+        except OSError as error:
+            raise NativeLibraryError(f"failed to load {target}: {error}") from error
+        for name, restype, argtypes in SIGNATURES:
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = list(argtypes)
+        if path is None:
+            _lib = lib
+        return lib
+
+
+def library_loaded() -> bool:
+    return _lib is not None
+
+
+def _check(name: str, status: int) -> None:
+    if status != ENC_OK:
+        message = load_library().enc_last_error().decode("utf-8", "replace")
+        raise EncoderKernelError(name, status, message)
+
+
+def _ptr(tensor: Optional[torch.Tensor]) -> Optional[int]:
+    return None if tensor is None else tensor.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _require(tensor: torch.Tensor, name: str, dtype: torch.dtype) -> None:
+    if tensor.device.type != "cuda":
+        raise ValueError(f"{name} must be a CUDA (HIP) tensor")
+    if tensor.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {tensor.dtype}")
+    if not tensor.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def layernorm(
+    x: torch.Tensor,
+    weight: torch.Tensor,
+    bias: torch.Tensor,
+    eps: float,
+    out: Optional[torch.Tensor] = None,
+    row_mask: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """bf16 LayerNorm over the last dimension (enc_layernorm_bf16)."""
+    for tensor, name in ((x, "x"), (weight, "weight"), (bias, "bias")):
+        _require(tensor, name, torch.bfloat16)
+    width = x.shape[-1]
+    if weight.numel() != width or bias.numel() != width:
+        raise ValueError("weight and bias must have x.shape[-1] elements")
+    out = torch.empty_like(x) if out is None else out
+    mask = None
+    if row_mask is not None:
+        mask = row_mask.contiguous().view(torch.uint8)
+        if mask.numel() != x.numel() // width:
+            raise ValueError("row_mask must have one entry per row")
+    _check(
+        "enc_layernorm_bf16",
+        load_library().enc_layernorm_bf16(
+            x.data_ptr(), weight.data_ptr(), bias.data_ptr(), out.data_ptr(),
+            x.numel() // width, width, float(eps), _ptr(mask), _stream(x.device),
+        ),
+    )
+    return out
+
+
+def linear(
+    a: torch.Tensor,
+    weight: torch.Tensor,
+    bias: torch.Tensor,
+    epilogue: int = ENC_EPI_BIAS,
+    residual: Optional[torch.Tensor] = None,
+    row_mask: Optional[torch.Tensor] = None,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """epilogue(a . weight^T + bias) on MFMA (enc_linear_bf16)."""
+    for tensor, name in ((a, "a"), (weight, "weight"), (bias, "bias")):
+        _require(tensor, name, torch.bfloat16)
+    n, k = weight.shape
+    if a.shape[-1] != k or bias.numel() != n:
+        raise ValueError(f"shape mismatch: a {tuple(a.shape)}, weight {tuple(weight.shape)}")
+    rows = a.numel() // k
+    out = torch.empty((*a.shape[:-1], n), device=a.device, dtype=a.dtype) if out is None else out
+    if residual is not None:
+        _require(residual, "residual", torch.bfloat16)
+        if residual.shape != out.shape:
+            raise ValueError("residual must have the output shape")
+    mask = None if row_mask is None else row_mask.contiguous().view(torch.uint8)
+    _check(
+        "enc_linear_bf16",
+        load_library().enc_linear_bf16(
+            a.data_ptr(), weight.data_ptr(), bias.data_ptr(), _ptr(residual), out.data_ptr(),
+            rows, n, k, int(epilogue), _ptr(mask), _stream(a.device),
+        ),
+    )
+    return out
+
+
+def vt_stride(seq_len: int) -> int:
+    """Row stride of the transposed-V buffer: seq_len rounded up to 8."""
+    return (seq_len + 7) // 8 * 8
+
+
+def qkv_proj(
+    x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, num_heads: int
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Packed QKV projection; returns q, k [B,H,S,hd] and v_t [B,H,hd,ld_vt]."""
+    for tensor, name in ((x, "x"), (weight, "weight"), (bias, "bias")):
+        _require(tensor, name, torch.bfloat16)
+    batch, seq_len, d_model = x.shape
+    if tuple(weight.shape) != (3 * d_model, d_model) or bias.numel() != 3 * d_model:
+        raise ValueError("qkv weight must be [3*d_model, d_model] with a [3*d_model] bias")
+    hd = d_model // num_heads
+    q = torch.empty((batch, num_heads, seq_len, hd), device=x.device, dtype=x.dtype)
+    k = torch.empty_like(q)
+    v_t = torch.empty((batch, num_heads, hd, vt_stride(seq_len)), device=x.device, dtype=x.dtype)
+    _check(
+        "enc_qkv_proj_bf16",
+        load_library().enc_qkv_proj_bf16(
+            x.data_ptr(), weight.data_ptr(), bias.data_ptr(), q.data_ptr(), k.data_ptr(),
+            v_t.data_ptr(), batch, seq_len, d_model, num_heads, _stream(x.device),
+        ),
+    )
+    return q, k, v_t
+
+
+def attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v_t: torch.Tensor,
+    scale: float,
+    causal: bool,
+    kv_len: Optional[torch.Tensor] = None,
+    key_mask: Optional[torch.Tensor] = None,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Streaming attention; returns context [B, S, H*hd] (enc_attention_fwd_bf16)."""
+    for tensor, name in ((q, "q"), (k, "k"), (v_t, "v_t")):
+        _require(tensor, name, torch.bfloat16)
+    batch, heads, seq_len, hd = q.shape
+    if tuple(k.shape) != tuple(q.shape):
+        raise ValueError("q and k must have the same shape")
+    if tuple(v_t.shape) != (batch, heads, hd, vt_stride(seq_len)):
+        raise ValueError("v_t must be [B, H, hd, round_up(S, 8)]")
+    out = (
+        torch.empty((batch, seq_len, heads * hd), device=q.device, dtype=q.dtype)
+        if out is None
+        else out
+    )
+    if kv_len is not None:
+        _require(kv_len, "kv_len", torch.int32)
+    mask = None if key_mask is None else key_mask.contiguous().view(torch.uint8)
+    _check(
+        "enc_attention_fwd_bf16",
+        load_library().enc_attention_fwd_bf16(
+            q.data_ptr(), k.data_ptr(), v_t.data_ptr(), out.data_ptr(), batch, heads, seq_len, hd,
+            float(scale), int(bool(causal)), _ptr(kv_len), _ptr(mask), _stream(q.device),
+        ),
+    )
+    return out
+
+
+def mask_lengths(mask: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Per-row count of valid tokens of a [B, S] bool mask, as int32 on device."""
+    if mask.device.type != "cuda" or mask.dtype != torch.bool or mask.dim() != 2:
+        raise ValueError("mask must be a [B, S] bool CUDA tensor")
+    mask = mask.contiguous()
+    batch, seq_len = mask.shape
+    out = torch.empty((batch,), device=mask.device, dtype=torch.int32) if out is None else out
+    _check(
+        "enc_mask_lengths",
+        load_library().enc_mask_lengths(
+            mask.view(torch.uint8).data_ptr(), batch, seq_len, out.data_ptr(), _stream(mask.device)
+        ),
+    )
+    return out
+
+
+def encoder_workspace_bytes(batch: int, seq_len: int, d_model: int, num_heads: int, ffn_dim: int) -> int:
+    size = load_library().enc_encoder_workspace_bytes(batch, seq_len, d_model, num_heads, ffn_dim)
+    if size < 0:
+        raise ValueError("invalid encoder shape")
+    return int(size)
+
+
+def encoder_forward(
+    x: torch.Tensor,
+    out: torch.Tensor,
+    workspace: torch.Tensor,
+    weight_table: torch.Tensor,
+    num_heads: int,
+    ffn_dim: int,
+    num_layers: int,
+    eps: float,
+    causal: bool,
+    kv_len: Optional[torch.Tensor],
+    key_mask: Optional[torch.Tensor],
+    row_mask: Optional[torch.Tensor],
+) -> None:
+    """Run the whole encoder through enc_encoder_forward_bf16.
+
+    ``weight_table`` is a CPU int64 tensor of device pointers in the order the
+    C ABI documents; ``key_mask``/``row_mask`` are uint8 [B, S] tensors.
+    """
+    batch, seq_len, d_model = x.shape
+    table = ctypes.cast(weight_table.data_ptr(), ctypes.c_void_p)
+    _check(
+        "enc_encoder_forward_bf16",
+        load_library().enc_encoder_forward_bf16(
+            x.data_ptr(), out.data_ptr(), workspace.data_ptr(), workspace.numel(), table.value,
+            batch, seq_len, d_model, num_heads, ffn_dim, num_layers, float(eps), int(bool(causal)),
+            _ptr(kv_len), _ptr(key_mask), _ptr(row_mask), _stream(x.device),
+        ),
+    )
