@@ -53,7 +53,9 @@ const char* enc_last_error(void);
 /* LayerNorm over the last dimension with fp32 statistics:
  *   y[r, :] = bf16(gamma * ((x[r, :] - mean) * rsqrt(var + eps)) + beta)
  * If row_mask is non-null, rows with row_mask[r] == 0 are written as zeros
- * (the masked_fill that follows final_norm).  width % 64 == 0, width <= 4096.
+ * (the masked_fill that follows final_norm).  width is a power of two in
+ * [256, 4096].  The statistics follow torch's ROCm LayerNorm operation for
+ * operation, so the bf16 output equals nn.LayerNorm's bit for bit.
  * Replaces nn.LayerNorm at transformer_benchmark/models.py:721,723,907 and the
  * case-6 kernel wrapper transformer_benchmark/case6_exact_layer_norm.py:98-121
  * (kernel host function case6_exact_layer_norm.cu:157-198). */
@@ -78,7 +80,8 @@ int enc_linear_bf16(const void* a, const void* weight, const void* bias,
 /* Packed QKV projection x[batch*seq_len, d_model] . qkv_weight[3*d_model,
  * d_model]^T + qkv_bias, rounded to bf16 and written head-major:
  *   q, k : [batch, num_heads, seq_len, head_dim]
- *   v_t  : [batch, num_heads, head_dim, seq_len]   (V transposed per head)
+ *   v_t  : [batch, num_heads, head_dim, round_up(seq_len, 8)]  (V transposed
+ *          per head; the padding columns are never read)
  * head_dim = d_model / num_heads.  Replaces the packed projection and
  * .contiguous() head split of transformer_benchmark/models.py:160-240 and the
  * direct-layout wrapper direct_qkv.py:110-187 (baseline: models.py:35-53). */
@@ -87,16 +90,19 @@ int enc_qkv_proj_bf16(const void* x, const void* weight, const void* bias,
                       int64_t seq_len, int64_t d_model, int64_t num_heads,
                       void* stream);
 
-/* Streaming (online-softmax) attention; scores are never materialised.
+/* Streaming attention; scores are never materialised.
  * For each (b, h, query i), over keys j that are allowed:
  *   s_ij = bf16(bf16(q_i . k_j) * scale)
- *   p_ij = softmax_j(s_ij) in fp32 ;  context = bf16(sum_j bf16(p_ij) v_j)
+ *   p_ij = bf16(softmax_j(s_ij)) in fp32 ;  context = bf16(sum_j p_ij v_j)
+ * bit for bit as the reference computes them with torch on ROCm (the softmax
+ * max/sum/divide follow torch's reduction order).  seq_len above 2048 must be
+ * a multiple of 4.
  * Key j is excluded when causal and j > i, when kv_len is non-null and
  * j >= kv_len[b] (prefix padding), or when key_mask is non-null and
  * key_mask[b, j] == 0.  With kv_len, query rows i >= kv_len[b] are padding and
  * are written as zeros.  A query row with no allowed key is written as zeros.
  * context: [batch, seq_len, num_heads * head_dim] (token-major, the layout
- * out_proj consumes).  head_dim == 64.
+ * out_proj consumes).  head_dim == 64; v_t as produced by enc_qkv_proj_bf16.
  * Replaces transformer_benchmark/models.py:55-75 (baseline) and the
  * candidate's score/softmax/PV kernels: triangular_scores.py:110-291,
  * pv_context.py:79-542, native_softmax_bf16.py:129-184,

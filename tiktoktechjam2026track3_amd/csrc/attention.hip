@@ -1,35 +1,41 @@
-// Streaming multi-head attention forward for gfx950, head_dim = 64.
+// Streaming multi-head attention forward for gfx950, head_dim = 64, bitwise
+// equal to the reference's materialised softmax attention.
 //
 // Scores are never materialised: each workgroup owns BQ = 128 query rows of one
-// (batch, head) and streams 64-key tiles of K (and V^T) through LDS.
-//
-// Both products put the query index on the MFMA N dimension (the lane index),
-// so every per-query quantity lives in the lane that owns that query:
+// (batch, head) (32 per wavefront) and streams 64-key tiles of K (and V^T)
+// through double-buffered LDS.  Both products put the query on the MFMA N
+// dimension (the lane), so every per-query quantity lives in the lane that owns
+// the query (lane l: query l%32, key half l/32):
 //   S^T[key, q]  = K[key, :] . Q[q, :]        A = K tile (LDS), B = Q (registers)
 //   O^T[d, q]   += V^T[d, key] . P^T[key, q]  A = V^T tile (LDS), B = P (registers)
-// With the 32x32x16 accumulator layout (col = lane%32, row = 8*(r/4) + 4*(lane/32)
-// + r%4), lane l holds query l%32 and keys {8i + 4(l/32) + j}.  Those scores are
-// fed straight back as the B operand of the PV product: the MFMA reduction index
-// k is mapped to keys by the same permutation, so the V^T operand reads keys
-// {16kk + 4(l/32) + j} and {16kk + 8 + 4(l/32) + j} (two 8-byte LDS reads).
-// V arrives transposed ([B, H, hd, S]) from the QKV projection epilogue.
+// The K fragment's MFMA row r is fed key perm(r) = 16(i>>1) + 8h + 4(i&1) + j for
+// r = 8i + 4h + j, which leaves lane half h holding, for each 16-key group kk,
+// keys 16kk + 8h + e (e = 0..7) in consecutive accumulator registers: exactly the
+// B operand of the PV MFMA with the reduction index in natural key order, so PV
+// accumulates keys in the same order as the reference's matmul(P, V).
 //
-// Numerics reproduce the reference forward (transformer_benchmark/models.py:55-70)
-// rounding for rounding:
-//   s = bf16(bf16(q.k) * scale)          (the second rounding is exact for 1/8)
-//   p = bf16(exp(s - max_j s) / sum_j exp(s - max_j s))   fp32 softmax, then bf16
-//   context = bf16(sum_j p_j v_j)        fp32 accumulation in key order
-// Because p is rounded only after normalisation, the softmax takes two passes
-// over the keys: pass 1 streams K and computes each row's max and sum; pass 2
-// streams K and V^T, recomputes the scores, forms the final bf16 probabilities
-// and accumulates PV with no rescaling.  (A one-pass online softmax rounds
-// un-normalised probabilities instead, which changes almost every probability's
-// rounding and, through the residual stream, moves outputs past the bf16 gate.)
+// Numerics reproduce transformer_benchmark/models.py:55-70 bit for bit:
+//   s = bf16(bf16(q.k) * scale)                 (MFMA, fp32 accumulate, rounded)
+//   p = bf16(expf(s - max) / sum)               (torch.softmax in fp32, then bf16)
+//   context = bf16(sum_j p_j v_j)               (MFMA, fp32 accumulate)
+// The softmax sum is accumulated in the order torch's ROCm softmax uses:
+//   rows of <= 2048 keys (persistent warp softmax): "lane" lam = key % 64 sums its
+//     keys lam, lam+64, ... in order, then a 64-lane butterfly;
+//   longer rows (block softmax): "thread" t of 512 sums the 4-key vectors t,
+//     t+512, ... in order, then a shuffle-down tree inside each 64-thread warp and
+//     a tree over the 8 warp sums.
+// Both orders were pinned against torch.softmax on an MI355X by fingerprinting
+// the reduction tree.  Because p is rounded after normalisation, the kernel
+// sweeps the keys three times: (A) row max, (B) row sum, (C) probabilities + PV.
+// In sweep B for long rows, tiles are visited residue-major (tile n = r + 32m,
+// r = 0..31) so each 512-thread "thread" partial is completed in key order and
+// each warp's 64 partials are live in registers only while that warp is summed.
 //
 // Tile skipping: with causal masking a workgroup stops at the last key tile its
-// last query can see, and a wavefront skips the MFMAs of tiles entirely in its
-// future; with prefix padding (kv_len) key tiles past kv_len are never loaded
-// and query tiles past kv_len are written as zeros without any work.
+// last query can see, and a wavefront skips the MFMAs of tiles in its future;
+// with prefix padding (kv_len) key tiles past kv_len are never loaded and query
+// tiles past kv_len are written as zeros.  Skipped keys contribute exp(-inf) = 0
+// in the reference, so skipping them is exact.
 #include "common.h"
 #include "kernels.h"
 
@@ -38,15 +44,22 @@ namespace enc {
 namespace {
 
 constexpr int kHd = 64;
-constexpr int kBQ = 128;   // queries per workgroup (32 per wavefront)
-constexpr int kBKV = 64;   // keys per tile
+constexpr int kBQ = 128;      // queries per workgroup (32 per wavefront)
+constexpr int kBKV = 64;      // keys per tile
 constexpr int kLds = 64 + 8;  // padded LDS row (elements)
 constexpr int kThreads = 256;
-constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kWarpSoftmaxMaxKeys = 2048;  // rows up to this length use the warp order
 
 enum MaskMode : int { kMaskNone = 0, kMaskPrefix = 1, kMaskBytes = 2 };
 
-template <bool CAUSAL, int MASK, bool POW2_SCALE>
+// key offset inside a 64-key tile held by accumulator register r of block kb32
+// in lane half h (see the permutation above)
+__device__ __forceinline__ int tile_key(int kb32, int r, int h) {
+  const int i = r >> 2, j = r & 3;
+  return 32 * kb32 + 16 * (i >> 1) + 8 * h + 4 * (i & 1) + j;
+}
+
+template <bool CAUSAL, int MASK, bool POW2_SCALE, bool BLOCK_ORDER>
 __global__ void __launch_bounds__(kThreads)
 attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
                      const bf16_t* __restrict__ Vt, bf16_t* __restrict__ ctx, int H, int S,
@@ -57,9 +70,9 @@ attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg
   __shared__ uint8_t sM[2][kBKV];
 
   // 1D grid.  Non-causal: consecutive workgroups are consecutive query tiles of
-  // one head, so the ~1000 resident workgroups stream the same K/V and share
-  // it in L2.  Causal: heads vary fastest and query tiles run last-to-first, so
-  // the heaviest tiles (which see the most keys) start first.
+  // one head, so the resident workgroups stream the same K/V and share it in L2.
+  // Causal: heads vary fastest and query tiles run last-to-first, so the
+  // heaviest tiles (which see the most keys) start first.
   const int id = blockIdx.x;
   const int num_bh = static_cast<int>(gridDim.x) / num_qblocks;
   int bh, qb;
@@ -119,6 +132,8 @@ attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg
       for (int e = 0; e < 8; ++e) qf[ks][e] = static_cast<__bf16>(0.f);
     }
   }
+  // MFMA row l32 of a 32-key block reads K row perm(l32)
+  const int krow = 16 * ((l32 >> 3) >> 1) + 8 * ((l32 >> 2) & 1) + 4 * ((l32 >> 3) & 1) + (l32 & 3);
 
   // Tile loader: K tile = 64 keys x 64 d (512 x 16B chunks), V^T tile = 64 d x
   // 64 keys (512 chunks); 256 threads -> 2 chunks of each per thread.
@@ -169,23 +184,28 @@ attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg
     }
   };
 
-  // Exponent arithmetic: with a power-of-two scale, s = bf16(q.k) * scale is
-  // exact, so s - max(s) = (r - max r) * scale with r = bf16(q.k) and
-  // exp(s - max) = exp2((r - max r) * (scale * log2 e)), both factors exact.
-  // Otherwise s is rounded again after the scale and differences are taken in s.
-  const float cexp = POW2_SCALE ? scale * kLog2e : kLog2e;
-  auto score_value = [&](float raw) -> float {
-    const float r = round_bf16(raw);
-    if constexpr (POW2_SCALE) return r;
-    else return round_bf16(r * scale);
+  // Runs body(buf, tile) over nkb tiles in the order seq(0), seq(1), ...,
+  // double-buffered: the loads of the next tile overlap the current body.
+  auto sweep = [&](auto seq, bool with_v, auto body) {
+    if (nkb > 0) {
+      load_tile(seq(0), with_v);
+      store_tile(0, with_v);
+    }
+    __syncthreads();
+    for (int it = 0; it < nkb; ++it) {
+      const int cur = it & 1;
+      if (it + 1 < nkb) load_tile(seq(it + 1), with_v);
+      body(cur, seq(it));
+      if (it + 1 < nkb) store_tile(cur ^ 1, with_v);
+      __syncthreads();
+    }
   };
 
-  // The wavefront's query rows; key tiles with k0 > wq_last are in its future.
   const int wq_first = q0 + wave * 32;
   const int wq_last = wq_first + 31;
 
-  // S^T tile (64 keys x 32 queries) of the current LDS buffer into s[2], already
-  // converted to score values, excluded keys set to -inf.
+  // Score tile (64 keys x 32 queries) of LDS buffer `buf` into s[2]: the
+  // reference's fp32 view of its bf16 scores, excluded keys = -inf.
   auto tile_scores = [&](int buf, int k0, f32x16 (&s)[2]) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -197,7 +217,7 @@ attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         const bf16x8 kf = *reinterpret_cast<const bf16x8*>(
-            &sK[buf][(kb32 * 32 + l32) * kLds + ks * 16 + lhi * 8]);
+            &sK[buf][(kb32 * 32 + krow) * kLds + ks * 16 + lhi * 8]);
         s[kb32] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], s[kb32], 0, 0, 0);
       }
     }
@@ -207,9 +227,10 @@ attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg
     for (int kb32 = 0; kb32 < 2; ++kb32) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        float v = score_value(s[kb32][r]);
+        const float rq = round_bf16(s[kb32][r]);
+        float v = POW2_SCALE ? rq * scale : round_bf16(rq * scale);
         if (need_mask) {
-          const int kl = kb32 * 32 + 8 * (r >> 2) + 4 * lhi + (r & 3);
+          const int kl = tile_key(kb32, r, lhi);
           const int key = k0 + kl;
           bool ok = key < kv_limit;
           if constexpr (CAUSAL) ok = ok && key <= qrow;
@@ -220,98 +241,174 @@ attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg
       }
     }
   };
+  auto natural = [](int it) { return it; };
 
-  // ================= pass 1: row max and row sum of exp(s - max) =================
-  // Each lane keeps its own running max/sum over its half of the keys; the two
-  // halves (lanes l and l^32) are merged once at the end.
+  // ============================ sweep A: row max ============================
   float m_lane = -INFINITY;
-  float l_lane = 0.f;
-  if (nkb > 0) {
-    load_tile(0, false);
-    store_tile(0, false);
-  }
-  __syncthreads();
-  for (int kb = 0; kb < nkb; ++kb) {
-    const int cur = kb & 1;
-    if (kb + 1 < nkb) load_tile(kb + 1, false);
+  sweep(natural, false, [&](int buf, int kb) {
     const int k0 = kb * kBKV;
-    if (!CAUSAL || k0 <= wq_last) {
-      f32x16 s[2];
-      tile_scores(cur, k0, s);
-      float mx = -INFINITY;
+    if (CAUSAL && k0 > wq_last) return;
+    f32x16 s[2];
+    tile_scores(buf, k0, s);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fmaxf(s[0][r], s[1][r]));
-      const float m_new = fmaxf(m_lane, mx);
-      const float base = (m_new == -INFINITY) ? 0.f : m_new;
-      float acc = l_lane * exp2f((m_lane - base) * cexp);
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        acc += exp2f((s[0][r] - base) * cexp);
-        acc += exp2f((s[1][r] - base) * cexp);
-      }
-      l_lane = acc;
-      m_lane = m_new;
-    }
-    if (kb + 1 < nkb) store_tile(cur ^ 1, false);
-    __syncthreads();
-  }
-  const float m_other = __shfl_xor(m_lane, 32, kWave);
-  const float l_other = __shfl_xor(l_lane, 32, kWave);
-  const float m_row = fmaxf(m_lane, m_other);
-  const float base = (m_row == -INFINITY) ? 0.f : m_row;
-  const float l_row = l_lane * exp2f((m_lane - base) * cexp) + l_other * exp2f((m_other - base) * cexp);
-  const float inv_l = (l_row > 0.f) ? 1.0f / l_row : 0.f;
+    for (int r = 0; r < 16; ++r) m_lane = fmaxf(m_lane, fmaxf(s[0][r], s[1][r]));
+  });
+  const float row_max = fmaxf(m_lane, __shfl_xor(m_lane, 32, kWave));
 
-  // ========== pass 2: p = bf16(exp(s - max) / sum), context = sum_j p_j v_j ==========
-  // P is final when it is rounded (as in the reference), so the PV product
-  // accumulates in plain key order with no rescaling.
+  // ======================= sweep B: row sum of expf(s - max) =======================
+  float row_sum;
+  if constexpr (!BLOCK_ORDER) {
+    // warp order: partial[lam] over keys lam, lam+64, ... (lam = key % 64)
+    float part[2][16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      part[0][r] = 0.f;
+      part[1][r] = 0.f;
+    }
+    sweep(natural, false, [&](int buf, int kb) {
+      const int k0 = kb * kBKV;
+      if (CAUSAL && k0 > wq_last) return;
+      f32x16 s[2];
+      tile_scores(buf, k0, s);
+#pragma unroll
+      for (int kb32 = 0; kb32 < 2; ++kb32)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) part[kb32][r] += expf(s[kb32][r] - row_max);
+    });
+    // 64-lane butterfly; lam bits: 5 = kb32, 4 = i>>1 (reg bit 3), 3 = lane half,
+    // 2 = i&1 (reg bit 2), 1..0 = j (reg bits 1..0)
+    float a[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) a[r] = part[0][r] + part[1][r];             // offset 32
+    float c[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) c[r] = a[r] + a[r + 8];                      // offset 16
+#pragma unroll
+    for (int r = 0; r < 8; ++r) c[r] = c[r] + __shfl_xor(c[r], 32, kWave);  // offset 8
+    float d4[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) d4[r] = c[r] + c[r + 4];                     // offset 4
+    const float e2a = d4[0] + d4[2], e2b = d4[1] + d4[3];                    // offset 2
+    row_sum = e2a + e2b;                                                     // offset 1
+  } else {
+    // block order: "thread" t (of 512) sums 4-key vectors t, t+512, ...; tile
+    // n = r + 32 m holds the vectors of threads 16 r .. 16 r + 15.  Tiles are
+    // visited residue-major; "warp" w covers residues 4w .. 4w+3.
+    auto resmajor = [&](int it) {
+      int r = 0;
+      int acc = 0;
+      while (true) {
+        const int cnt = (nkb - r + 31) / 32;  // tiles with residue r
+        if (it < acc + cnt) return r + 32 * (it - acc);
+        acc += cnt;
+        ++r;
+      }
+    };
+    float warp_sum[8];
+    float part[4][8];  // [residue within warp][vector slot 4*kb32 + i]
+#pragma unroll
+    for (int w = 0; w < 8; ++w) warp_sum[w] = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int v = 0; v < 8; ++v) part[q][v] = 0.f;
+    int cur_warp = 0;
+    auto flush_warp = [&](int w) {
+      // shuffle-down tree over lam = 16 rr + u, u = 8 kb32 + 4 (i>>1) + 2 h + (i&1):
+      // offsets 32, 16 (rr), 8 (kb32), 4 (i>>1), 2 (lane half), 1 (i&1)
+      float t8[8];
+#pragma unroll
+      for (int v = 0; v < 8; ++v) t8[v] = (part[0][v] + part[2][v]) + (part[1][v] + part[3][v]);
+      float t4[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) t4[v] = t8[v] + t8[v + 4];                   // offset 8 (kb32)
+      float t2[2];
+#pragma unroll
+      for (int v = 0; v < 2; ++v) t2[v] = t4[v] + t4[v + 2];                   // offset 4 (i>>1)
+#pragma unroll
+      for (int v = 0; v < 2; ++v) t2[v] = t2[v] + __shfl_xor(t2[v], 32, kWave);  // offset 2
+      const float ws = t2[0] + t2[1];                                          // offset 1 (i&1)
+#pragma unroll
+      for (int ww = 0; ww < 8; ++ww)
+        if (ww == w) warp_sum[ww] = ws;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int v = 0; v < 8; ++v) part[q][v] = 0.f;
+    };
+    sweep(resmajor, false, [&](int buf, int kb) {
+      const int k0 = kb * kBKV;
+      const int r = kb & 31;
+      const int w = r >> 2;
+      while (cur_warp < w) {  // warps whose residues are complete are reduced
+        flush_warp(cur_warp);
+        ++cur_warp;
+      }
+      if (CAUSAL && k0 > wq_last) return;
+      f32x16 s[2];
+      tile_scores(buf, k0, s);
+      const int rr = r & 3;
+#pragma unroll
+      for (int kb32 = 0; kb32 < 2; ++kb32) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float acc = 0.f;
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (q == rr) acc = part[q][4 * kb32 + i];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc += expf(s[kb32][4 * i + j] - row_max);
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (q == rr) part[q][4 * kb32 + i] = acc;
+        }
+      }
+    });
+    while (cur_warp < 8) {
+      flush_warp(cur_warp);
+      ++cur_warp;
+    }
+    // tree over the 8 warp sums (offsets 4, 2, 1)
+    const float a0 = warp_sum[0] + warp_sum[4], a1 = warp_sum[1] + warp_sum[5];
+    const float a2 = warp_sum[2] + warp_sum[6], a3 = warp_sum[3] + warp_sum[7];
+    row_sum = (a0 + a2) + (a1 + a3);
+  }
+
+  // ============= sweep C: p = bf16(expf(s - max) / sum), context += P V =============
   f32x16 o[2];
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     o[0][r] = 0.f;
     o[1][r] = 0.f;
   }
-  if (nkb > 0) {
-    load_tile(0, true);
-    store_tile(0, true);
-  }
-  __syncthreads();
-  for (int kb = 0; kb < nkb; ++kb) {
-    const int cur = kb & 1;
-    if (kb + 1 < nkb) load_tile(kb + 1, true);
+  sweep(natural, true, [&](int buf, int kb) {
     const int k0 = kb * kBKV;
-    if (!CAUSAL || k0 <= wq_last) {
-      f32x16 s[2];
-      tile_scores(cur, k0, s);
-      bf16x8 pf[4];
+    if (CAUSAL && k0 > wq_last) return;
+    f32x16 s[2];
+    tile_scores(buf, k0, s);
+    bf16x8 pf[4];
 #pragma unroll
-      for (int kb32 = 0; kb32 < 2; ++kb32) {
+    for (int kb32 = 0; kb32 < 2; ++kb32) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float p = exp2f((s[kb32][r] - base) * cexp) * inv_l;
-          pf[kb32 * 2 + (r >> 3)][r & 7] = static_cast<__bf16>(p);
-        }
-      }
-#pragma unroll
-      for (int db = 0; db < 2; ++db) {
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-          const bf16_t* vrow = &sV[cur][(db * 32 + l32) * kLds + 16 * kk + 4 * lhi];
-          const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow);
-          const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + 8);
-          const u32x4 vv = {lo[0], lo[1], hi[0], hi[1]};
-          const bf16x8 vf = __builtin_bit_cast(bf16x8, vv);
-          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[kk], o[db], 0, 0, 0);
-        }
+      for (int r = 0; r < 16; ++r) {
+        const float p = expf(s[kb32][r] - row_max) / row_sum;
+        pf[kb32 * 2 + (r >> 3)][r & 7] = static_cast<__bf16>(p);
       }
     }
-    if (kb + 1 < nkb) store_tile(cur ^ 1, true);
-    __syncthreads();
-  }
+#pragma unroll
+    for (int db = 0; db < 2; ++db) {
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const bf16x8 vf = *reinterpret_cast<const bf16x8*>(
+            &sV[buf][(db * 32 + l32) * kLds + 16 * kk + 8 * lhi]);
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[kk], o[db], 0, 0, 0);
+      }
+    }
+  });
 
   // ---- write context[b, qrow, h*64 + d] = bf16(O) ----
   if (qrow < S) {
-    bool zero = !(l_row > 0.f);
+    bool zero = !(row_sum > 0.f);
     if constexpr (MASK == kMaskPrefix) zero = zero || qrow >= kv_limit;
 #pragma unroll
     for (int db = 0; db < 2; ++db) {
@@ -329,24 +426,33 @@ attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg
   }
 }
 
-template <bool CAUSAL, int MASK, bool POW2>
+template <bool CAUSAL, int MASK, bool POW2, bool BLOCK_ORDER>
 hipError_t launch_attn(const bf16_t* q, const bf16_t* k, const bf16_t* vt, bf16_t* ctx, int B,
                        int H, int S, float scale, const int32_t* kv_len, const uint8_t* key_mask,
                        hipStream_t st) {
   const int nqb = (S + kBQ - 1) / kBQ;
   const dim3 grid(static_cast<uint32_t>(B) * H * nqb);
   const int ld_vt = static_cast<int>(vt_stride(S));
-  hipLaunchKernelGGL((attn_fwd_hd64_kernel<CAUSAL, MASK, POW2>), grid, dim3(kThreads), 0, st, q,
-                     k, vt, ctx, H, S, ld_vt, nqb, scale, kv_len, key_mask);
+  hipLaunchKernelGGL((attn_fwd_hd64_kernel<CAUSAL, MASK, POW2, BLOCK_ORDER>), grid, dim3(kThreads),
+                     0, st, q, k, vt, ctx, H, S, ld_vt, nqb, scale, kv_len, key_mask);
   return hipGetLastError();
+}
+
+template <bool CAUSAL, int MASK, bool POW2>
+hipError_t dispatch_order(const bf16_t* q, const bf16_t* k, const bf16_t* vt, bf16_t* ctx, int B,
+                          int H, int S, float scale, const int32_t* kv_len,
+                          const uint8_t* key_mask, hipStream_t st) {
+  if (S > kWarpSoftmaxMaxKeys)
+    return launch_attn<CAUSAL, MASK, POW2, true>(q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
+  return launch_attn<CAUSAL, MASK, POW2, false>(q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
 }
 
 template <bool CAUSAL, int MASK>
 hipError_t dispatch_pow2(bool pow2, const bf16_t* q, const bf16_t* k, const bf16_t* vt,
                          bf16_t* ctx, int B, int H, int S, float scale, const int32_t* kv_len,
                          const uint8_t* key_mask, hipStream_t st) {
-  if (pow2) return launch_attn<CAUSAL, MASK, true>(q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
-  return launch_attn<CAUSAL, MASK, false>(q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
+  if (pow2) return dispatch_order<CAUSAL, MASK, true>(q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
+  return dispatch_order<CAUSAL, MASK, false>(q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
 }
 
 template <bool CAUSAL>
@@ -373,6 +479,11 @@ mask_lengths_kernel(const uint8_t* __restrict__ mask, int64_t S, int32_t* __rest
 }
 
 }  // namespace
+
+bool attention_seq_supported(int64_t seq_len) {
+  // torch's long-row softmax folds 4-element vectors; other lengths are not pinned
+  return seq_len <= kWarpSoftmaxMaxKeys || seq_len % 4 == 0;
+}
 
 hipError_t attention_fwd_bf16(const bf16_t* q, const bf16_t* k, const bf16_t* v_t, bf16_t* ctx,
                               int batch, int heads, int seq_len, int head_dim, float scale,

@@ -89,8 +89,11 @@ int check_encoder_shape(int64_t B, int64_t S, int64_t D, int64_t H, int64_t F) {
     return fail(ENC_ERR_UNSUPPORTED, "attention kernel supports head_dim == 64 only (got " +
                                          std::to_string(D / H) + ")");
   if (!enc::layernorm_supported(D))
-    return fail(ENC_ERR_UNSUPPORTED, "LayerNorm width must be a power of two in [64, 4096] (got " +
+    return fail(ENC_ERR_UNSUPPORTED, "LayerNorm width must be a power of two in [256, 4096] (got " +
                                          std::to_string(D) + ")");
+  if (!enc::attention_seq_supported(S))
+    return fail(ENC_ERR_UNSUPPORTED, "seq_len above 2048 must be a multiple of 4 (got " +
+                                         std::to_string(S) + ")");
   if (D % 64 != 0 || F % 64 != 0)
     return fail(ENC_ERR_UNSUPPORTED, "d_model and ffn_dim must be multiples of 64");
   if (B * S >= (int64_t(1) << 31)) return fail(ENC_ERR_UNSUPPORTED, "batch * seq_len must be < 2^31");
@@ -111,7 +114,7 @@ int enc_layernorm_bf16(const void* x, const void* gamma, const void* beta, void*
   if (rows == 0) return ok();
   if (!x || !gamma || !beta || !y) return fail(ENC_ERR_INVALID, "layernorm: null tensor pointer");
   if (!enc::layernorm_supported(width))
-    return fail(ENC_ERR_UNSUPPORTED, "layernorm: width must be a power of two in [64, 4096]");
+    return fail(ENC_ERR_UNSUPPORTED, "layernorm: width must be a power of two in [256, 4096]");
   if (!(eps > 0.f)) return fail(ENC_ERR_INVALID, "layernorm: eps must be positive");
   hipError_t e = enc::layernorm_bf16(static_cast<const enc::bf16_t*>(x), static_cast<const enc::bf16_t*>(gamma),
                                      static_cast<const enc::bf16_t*>(beta), static_cast<enc::bf16_t*>(y), rows,
@@ -183,6 +186,8 @@ int enc_attention_fwd_bf16(const void* q, const void* k, const void* v_t, void* 
   if (head_dim != 64) return fail(ENC_ERR_UNSUPPORTED, "attention: head_dim must be 64");
   if (kv_len && key_mask) return fail(ENC_ERR_INVALID, "attention: pass kv_len or key_mask, not both");
   if (!(scale > 0.f)) return fail(ENC_ERR_INVALID, "attention: scale must be positive");
+  if (!enc::attention_seq_supported(seq_len))
+    return fail(ENC_ERR_UNSUPPORTED, "attention: seq_len above 2048 must be a multiple of 4");
   if (batch * num_heads * ((seq_len + 127) / 128) >= (int64_t(1) << 31))
     return fail(ENC_ERR_UNSUPPORTED, "attention: grid too large");
   hipError_t e = enc::attention_fwd_bf16(

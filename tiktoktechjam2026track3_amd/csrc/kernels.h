@@ -54,6 +54,9 @@ hipError_t attention_fwd_bf16(const bf16_t* q, const bf16_t* k, const bf16_t* v_
                               bool causal, const int32_t* kv_len, const uint8_t* key_mask,
                               hipStream_t stream);
 
+// Sequence lengths whose softmax summation order is reproduced exactly.
+bool attention_seq_supported(int64_t seq_len);
+
 hipError_t mask_lengths(const uint8_t* mask, int64_t batch, int64_t seq_len, int32_t* kv_len,
                         hipStream_t stream);
 

@@ -413,8 +413,11 @@ class UserOptimizedTransformer(BaselineTransformer):
         problems = []
         if hd != 64:
             problems.append(f"head_dim {hd} (supported: 64)")
-        if cfg.d_model not in (64, 128, 256, 512, 1024, 2048, 4096):
-            problems.append(f"d_model {cfg.d_model} (supported: powers of two 64..4096)")
+        if cfg.d_model not in (256, 512, 1024, 2048, 4096):
+            problems.append(f"d_model {cfg.d_model} (supported: powers of two 256..4096)")
+        seq_len = x.shape[1]
+        if seq_len > 2048 and seq_len % 4:
+            problems.append(f"seq_len {seq_len} (above 2048 it must be a multiple of 4)")
         if cfg.ffn_dim % 64 != 0:
             problems.append(f"ffn_dim {cfg.ffn_dim} (must be a multiple of 64)")
         if problems:
