@@ -76,12 +76,21 @@ __device__ __forceinline__ void store_row_major(const GemmEpilogueArgs& ep, int 
   }
 }
 
-template <int BM, int BN, int EPI>
+// SPLIT > 1 reproduces the K-split reduction order hipBLASLt picks for some
+// small-M shapes: the K range is cut into CW-wide chunks, chunk c is accumulated
+// into partial (c % SPLIT) in ascending order, and the partials are added
+// left to right before the bias.  All partials live in registers of the same
+// wavefront, so the split costs registers, not a second pass.
+template <int BM, int BN, int EPI, int SPLIT = 1, int CW = kBK>
 __global__ void __launch_bounds__(kThreads)
 gemm_bf16_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int M, int N, int K,
                  GemmEpilogueArgs ep) {
   constexpr int RM = BM / 64;  // 32x32 blocks per wavefront along M
   constexpr int RN = BN / 64;  // ... along N
+  // K tiles after which the chunk -> partial assignment repeats (even, so the
+  // double-buffer index is also a compile-time value inside one period).
+  constexpr int PERIOD = (SPLIT == 1) ? 2 : ((CW * SPLIT / kBK) < 2 ? 2 : CW * SPLIT / kBK);
+  static_assert(SPLIT == 1 || (CW % 16 == 0 && (CW * SPLIT) % kBK == 0), "bad split chunk");
   constexpr int A_LOADS = BM * (kBK / 8) / kThreads;
   constexpr int B_LOADS = BN * (kBK / 8) / kThreads;
   static_assert(A_LOADS >= 1 && B_LOADS >= 1, "tile too small for 256 threads");
@@ -141,13 +150,15 @@ gemm_bf16_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int
     }
   };
 
-  f32x16 acc[RM][RN];
+  f32x16 acc[SPLIT][RM][RN];
 #pragma unroll
-  for (int i = 0; i < RM; ++i)
+  for (int p = 0; p < SPLIT; ++p)
 #pragma unroll
-    for (int j = 0; j < RN; ++j)
+    for (int i = 0; i < RM; ++i)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+      for (int j = 0; j < RN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[p][i][j][r] = 0.f;
 
   const int KT = K / kBK;
   load_global(0);
@@ -157,28 +168,44 @@ gemm_bf16_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int
   const int a_base = (wm * (BM / 2) + l32) * kLdk + lhi * 8;
   const int b_base = (wn * (BN / 2) + l32) * kLdk + lhi * 8;
 
-  for (int kt = 0; kt < KT; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < KT) load_global((kt + 1) * kBK);
+  // KT is a multiple of PERIOD except for SPLIT == 1, where the tail of the
+  // last period is skipped by the kt < KT test.
+  for (int kt0 = 0; kt0 < KT; kt0 += PERIOD) {
 #pragma unroll
-    for (int ks = 0; ks < kBK / 16; ++ks) {
-      bf16x8 af[RM];
-      bf16x8 bfr[RN];
+    for (int pt = 0; pt < PERIOD; ++pt) {
+      const int kt = kt0 + pt;
+      if (SPLIT == 1 && kt >= KT) break;
+      const int cur = pt & 1;
+      if (kt + 1 < KT) load_global((kt + 1) * kBK);
 #pragma unroll
-      for (int i = 0; i < RM; ++i)
-        af[i] = *reinterpret_cast<const bf16x8*>(&sA[cur][a_base + i * 32 * kLdk + ks * 16]);
+      for (int ks = 0; ks < kBK / 16; ++ks) {
+        const int part = SPLIT == 1 ? 0 : ((pt * kBK + ks * 16) / CW) % SPLIT;
+        bf16x8 af[RM];
+        bf16x8 bfr[RN];
 #pragma unroll
-      for (int j = 0; j < RN; ++j)
-        bfr[j] = *reinterpret_cast<const bf16x8*>(&sB[cur][b_base + j * 32 * kLdk + ks * 16]);
-#pragma unroll
-      for (int i = 0; i < RM; ++i)
+        for (int i = 0; i < RM; ++i)
+          af[i] = *reinterpret_cast<const bf16x8*>(&sA[cur][a_base + i * 32 * kLdk + ks * 16]);
 #pragma unroll
         for (int j = 0; j < RN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+          bfr[j] = *reinterpret_cast<const bf16x8*>(&sB[cur][b_base + j * 32 * kLdk + ks * 16]);
+#pragma unroll
+        for (int i = 0; i < RM; ++i)
+#pragma unroll
+          for (int j = 0; j < RN; ++j)
+            acc[part][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[part][i][j], 0, 0, 0);
+      }
+      if (kt + 1 < KT) store_lds(cur ^ 1);
+      __syncthreads();
     }
-    if (kt + 1 < KT) store_lds(cur ^ 1);
-    __syncthreads();
   }
+#pragma unroll
+  for (int p = 1; p < SPLIT; ++p)
+#pragma unroll
+    for (int i = 0; i < RM; ++i)
+#pragma unroll
+      for (int j = 0; j < RN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[0][i][j][r] += acc[p][i][j][r];
 
   // ---- epilogue ----
   const int row_base = m0 + wm * (BM / 2);
@@ -202,7 +229,7 @@ gemm_bf16_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int
           const int row0 = row_base + i * 32 + 8 * g + 4 * lhi;  // 4 consecutive rows
           float y[4];
 #pragma unroll
-          for (int jj = 0; jj < 4; ++jj) y[jj] = acc[i][j][4 * g + jj] + bias;
+          for (int jj = 0; jj < 4; ++jj) y[jj] = acc[0][i][j][4 * g + jj] + bias;
           if (which < 2) {
             bf16_t* dst = which == 0 ? ep.q : ep.k;
 #pragma unroll
@@ -241,7 +268,7 @@ gemm_bf16_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int row = row_base + i * 32 + 8 * (r >> 2) + 4 * lhi + (r & 3);
-          if (row < M) store_row_major<EPI>(ep, N, row, col, acc[i][j][r], bias);
+          if (row < M) store_row_major<EPI>(ep, N, row, col, acc[0][i][j][r], bias);
         }
       }
     }
@@ -286,7 +313,52 @@ hipError_t launch_tile(const bf16_t* A, const bf16_t* W, int M, int N, int K, in
   return hipGetLastError();
 }
 
+// K-split launches use the 64x64 tile: four partial accumulator sets still fit
+// the register budget there.
+template <int SPLIT, int CW>
+hipError_t launch_split(const bf16_t* A, const bf16_t* W, int M, int N, int K, int epi,
+                        const GemmEpilogueArgs& ep, hipStream_t st) {
+  const int tiles = ((M + 63) / 64) * (N / 64);
+  const dim3 grid(tiles), block(kThreads);
+  switch (epi) {
+    case kEpiBias: hipLaunchKernelGGL((gemm_bf16_kernel<64, 64, kEpiBias, SPLIT, CW>), grid, block, 0, st, A, W, M, N, K, ep); break;
+    case kEpiBiasGelu: hipLaunchKernelGGL((gemm_bf16_kernel<64, 64, kEpiBiasGelu, SPLIT, CW>), grid, block, 0, st, A, W, M, N, K, ep); break;
+    case kEpiResidualKeep: hipLaunchKernelGGL((gemm_bf16_kernel<64, 64, kEpiResidualKeep, SPLIT, CW>), grid, block, 0, st, A, W, M, N, K, ep); break;
+    case kEpiResidualZero: hipLaunchKernelGGL((gemm_bf16_kernel<64, 64, kEpiResidualZero, SPLIT, CW>), grid, block, 0, st, A, W, M, N, K, ep); break;
+    case kEpiQkvHeadMajor: hipLaunchKernelGGL((gemm_bf16_kernel<64, 64, kEpiQkvHeadMajor, SPLIT, CW>), grid, block, 0, st, A, W, M, N, K, ep); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 }  // namespace
+
+void gemm_split_plan(int64_t M, int64_t N, int64_t K, int* split, int* chunk) {
+  // The reduction order torch.nn.functional.linear (hipBLASLt on ROCm 7) uses
+  // for bf16 [M, K] x [N, K]^T, measured per shape with inputs whose rounding
+  // reveals which K indices share a partial sum.  Shapes not listed here
+  // accumulate K sequentially, which is what the unsplit kernel does.
+  struct Rule {
+    int64_t max_m, n, k;
+    int split, chunk;
+  };
+  static constexpr Rule kRules[] = {
+      {16, 512, 512, 4, 32},    {16, 512, 2048, 4, 32},   {16, 1536, 512, 4, 32},
+      {16, 2048, 512, 4, 32},   {16, 1024, 1024, 4, 32},  {16, 1024, 4096, 2, 128},
+      {16, 4096, 1024, 4, 32},  {16, 3072, 1024, 4, 32},  {64, 512, 2048, 4, 32},
+      {64, 1024, 4096, 2, 128}, {128, 512, 2048, 4, 32},  {128, 1024, 4096, 4, 64},
+      {256, 512, 2048, 4, 32},
+  };
+  *split = 1;
+  *chunk = kBK;
+  for (const Rule& r : kRules) {
+    if (M <= r.max_m && N == r.n && K == r.k) {
+      *split = r.split;
+      *chunk = r.chunk;
+      return;
+    }
+  }
+}
 
 void gemm_pick_tile(int64_t M, int64_t N, int epilogue, int num_cus, int* bm, int* bn) {
   double best = 1e300;
@@ -316,9 +388,14 @@ bool gemm_supported(int64_t M, int64_t N, int64_t K) {
 hipError_t gemm_bf16(const bf16_t* A, const bf16_t* W, int64_t M, int64_t N, int64_t K, int epi,
                      const GemmEpilogueArgs& ep, int num_cus, hipStream_t stream) {
   if (M == 0) return hipSuccess;
+  const int m = static_cast<int>(M), n = static_cast<int>(N), k = static_cast<int>(K);
+  int split, chunk;
+  gemm_split_plan(M, N, K, &split, &chunk);
+  if (split == 4 && chunk == 32) return launch_split<4, 32>(A, W, m, n, k, epi, ep, stream);
+  if (split == 4 && chunk == 64) return launch_split<4, 64>(A, W, m, n, k, epi, ep, stream);
+  if (split == 2 && chunk == 128) return launch_split<2, 128>(A, W, m, n, k, epi, ep, stream);
   int bm, bn;
   gemm_pick_tile(M, N, epi, num_cus, &bm, &bn);
-  const int m = static_cast<int>(M), n = static_cast<int>(N), k = static_cast<int>(K);
   if (bm == 256 && bn == 256) return launch_tile<256, 256>(A, W, m, n, k, epi, ep, stream);
   if (bm == 256 && bn == 128) return launch_tile<256, 128>(A, W, m, n, k, epi, ep, stream);
   if (bm == 128 && bn == 128) return launch_tile<128, 128>(A, W, m, n, k, epi, ep, stream);

@@ -47,6 +47,10 @@ hipError_t gemm_bf16(const bf16_t* A, const bf16_t* W, int64_t M, int64_t N, int
 
 // Tile shape the dispatcher picks for (M, N) on a device with num_cus CUs.
 void gemm_pick_tile(int64_t M, int64_t N, int epilogue, int num_cus, int* bm, int* bn);
+// K-split reduction order matching torch.nn.functional.linear for this shape:
+// split == 1 means sequential K; otherwise chunk-wide K chunks are accumulated
+// into partial (chunk index % split) and the partials are added in order.
+void gemm_split_plan(int64_t M, int64_t N, int64_t K, int* split, int* chunk);
 
 // Attention (head_dim 64).  v_t row stride is ld_vt = round_up(S, 8).
 hipError_t attention_fwd_bf16(const bf16_t* q, const bf16_t* k, const bf16_t* v_t, bf16_t* ctx,

@@ -8,15 +8,19 @@
 //   * the row is viewed as width/4 vectors of 4 elements; "virtual thread" t of
 //     a 256-thread block (4 warps x 64 lanes) folds vectors t, t+256, ... with
 //     Welford online updates  mean += delta * rcp(n);  m2 += delta * (x - mean)
-//     (hardware reciprocal, FMA on the mean update only);
+//     (FMA on the mean update only).  rcp is the hardware v_rcp_f32, which
+//     is not the correctly rounded 1/n for every n (1/3 comes out one ulp
+//     low), so it is issued through inline asm: with the counts known at
+//     compile time the builtin would be folded to the correctly rounded value;
 //   * each virtual warp is merged by a shuffle-down tree (offsets 32..1) of the
 //     Welford combine (count-weighted mean, m2 += delta^2 * nA * nB / n), then
 //     warps 0+2, 1+3 and 0+1;
 //   * var = m2 / width, rstd = rsqrt(var + eps), y = fma(gamma, rstd*(x-mean), beta).
 // Here lane l carries virtual threads l, l+64, l+128, l+192 (one per virtual
-// warp) and runs the four warp trees side by side.  The expression order was
-// pinned by comparing against torch's bf16 LayerNorm on an MI355X: 0 of
-// 6.1e7 outputs differ.
+// warp) and runs the four warp trees side by side.  The operation order was
+// pinned against torch's native_layer_norm on an MI355X: mean and rstd of
+// 4096 encoder activation rows (width 1024) and of 24576 rows built to expose
+// the merge order all agree bit for bit.
 #include "common.h"
 #include "kernels.h"
 
@@ -25,17 +29,23 @@ namespace enc {
 namespace {
 
 constexpr int kRowsPerBlock = 4;  // one row per wavefront, 4 wavefronts
-constexpr int kVirtualThreads = 256;
 
 struct Welford {
   float mean, m2, count;
 };
 
+// v_rcp_f32 of a value the compiler may know; the asm keeps it from folding.
+__device__ __forceinline__ float hw_rcp(float n) {
+  float r;
+  asm("v_rcp_f32 %0, %1" : "=v"(r) : "v"(n));
+  return r;
+}
+
 __device__ __forceinline__ Welford welford_add(Welford s, float x) {
 #pragma clang fp contract(off)
   const float delta = x - s.mean;
   const float n = s.count + 1.f;
-  const float mean = fmaf(delta, __builtin_amdgcn_rcpf(n), s.mean);
+  const float mean = fmaf(delta, hw_rcp(n), s.mean);
   const float m2 = s.m2 + delta * (x - mean);
   return {mean, m2, n};
 }
@@ -46,11 +56,11 @@ __device__ __forceinline__ Welford welford_merge(Welford b, Welford a) {
   const float delta = b.mean - a.mean;
   const float n = a.count + b.count;
   if (!(n > 0.f)) return {0.f, 0.f, n};
-  const float coef = __builtin_amdgcn_rcpf(n);
+  const float coef = hw_rcp(n);
   const float na = a.count * coef;
   const float nb = b.count * coef;
   const float mean = na * a.mean + nb * b.mean;
-  const float m2 = (a.m2 + b.m2) + delta * delta * a.count * nb;
+  const float m2 = fmaf(delta * delta * a.count, nb, a.m2 + b.m2);
   return {mean, m2, n};
 }
 
