@@ -136,7 +136,12 @@ def attention_rows(
 ) -> torch.Tensor:
     """Context for the query rows ``q_rows`` [B, H, R, hd] at sequence positions
     ``row_positions`` [R]: bf16(softmax_fp32(bf16(q k^T) * scale masked)) @ v."""
-    scores = torch.matmul(q_rows, k.transpose(-2, -1)) * scale
+    k_t = k.transpose(-2, -1)
+    if k_t.is_cuda:
+        # bf16 batched products with a transposed right operand are not run on
+        # the GPU; the contiguous copy holds the same values
+        k_t = k_t.contiguous()
+    scores = torch.matmul(q_rows, k_t) * scale
     if causal:
         keys = torch.arange(k.shape[-2], device=k.device)
         future = keys[None, :] > row_positions.to(k.device)[:, None]

@@ -256,6 +256,32 @@ def test_attention_prefix_padding(device, b, h, s, causal):
     assert torch.all(out[~valid] == 0)
 
 
+@pytest.mark.parametrize(
+    "b,h,s,causal,prefix",
+    [(1, 8, 128, False, False), (8, 16, 1024, True, False), (4, 16, 8192, True, True), (4, 16, 4096, False, False)],
+)
+def test_attention_config_shapes_bitwise(device, b, h, s, causal, prefix):
+    """At the benchmark configurations' shapes the reference's batched matmuls
+    accumulate K in the kernel's order and the softmax follows torch's
+    regime (warp softmax up to 2048 keys, block softmax with the hardware exp
+    beyond), so the context equals the oracle's bit for bit."""
+    q, k, v, v_t = _attention_inputs(device, b, h, s, 3 * s + h)
+    kv_len = mask = None
+    if prefix:
+        g = torch.Generator(device=device).manual_seed(s + 1)
+        lengths = torch.randint(s // 2, s + 1, (b,), generator=g, device=device)
+        mask = torch.arange(s, device=device)[None, :] < lengths[:, None]
+        kv_len = lengths.int()
+    out = native.attention(q, k, v_t, 0.125, causal, kv_len=kv_len)
+    ref = _oracle_context(q, k, v, causal, mask)
+    if mask is not None:
+        valid = mask[..., None].expand_as(out)
+        assert torch.equal(ref[valid], out[valid])
+        assert torch.all(out[~valid] == 0)
+    else:
+        assert torch.equal(ref, out)
+
+
 @pytest.mark.parametrize("causal", [False, True])
 def test_attention_general_mask(device, causal):
     b, h, s = 2, 4, 300

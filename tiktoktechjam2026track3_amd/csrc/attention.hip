@@ -16,8 +16,12 @@
 //
 // Numerics reproduce transformer_benchmark/models.py:55-70 bit for bit:
 //   s = bf16(bf16(q.k) * scale)                 (MFMA, fp32 accumulate, rounded)
-//   p = bf16(expf(s - max) / sum)               (torch.softmax in fp32, then bf16)
+//   p = bf16(softmax_fp32(s))                   (torch.softmax in fp32, then bf16)
 //   context = bf16(sum_j p_j v_j)               (MFMA, fp32 accumulate)
+// torch's ROCm softmax computes p differently for the two row-length regimes:
+//   rows of <= 2048 keys: e = expf(s - max) (libm-accurate), p = e / sum;
+//   longer rows:          e = exp2(rn(s - max) * log2(e)) on the hardware exp
+//                         unit, p = e * (1 / sum) with a correctly rounded 1 / sum.
 // The softmax sum is accumulated in the order torch's ROCm softmax uses:
 //   rows of <= 2048 keys (persistent warp softmax): "lane" lam = key % 64 sums its
 //     keys lam, lam+64, ... in order, then a 64-lane butterfly;
@@ -49,6 +53,17 @@ constexpr int kBKV = 64;      // keys per tile
 constexpr int kLds = 64 + 8;  // padded LDS row (elements)
 constexpr int kThreads = 256;
 constexpr int kWarpSoftmaxMaxKeys = 2048;  // rows up to this length use the warp order
+constexpr float kLog2e = 1.44269504088896340736f;
+
+// exp of (s - max) as the softmax of the given regime computes it.
+template <bool BLOCK_ORDER>
+__device__ __forceinline__ float softmax_exp(float x) {
+  if constexpr (BLOCK_ORDER) {
+    return __builtin_amdgcn_exp2f(x * kLog2e);
+  } else {
+    return expf(x);
+  }
+}
 
 enum MaskMode : int { kMaskNone = 0, kMaskPrefix = 1, kMaskBytes = 2 };
 
@@ -273,7 +288,7 @@ attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg
 #pragma unroll
       for (int kb32 = 0; kb32 < 2; ++kb32)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) part[kb32][r] += expf(s[kb32][r] - row_max);
+        for (int r = 0; r < 16; ++r) part[kb32][r] += softmax_exp<false>(s[kb32][r] - row_max);
     });
     // 64-lane butterfly; lam bits: 5 = kb32, 4 = i>>1 (reg bit 3), 3 = lane half,
     // 2 = i&1 (reg bit 2), 1..0 = j (reg bits 1..0)
@@ -357,7 +372,7 @@ attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg
           for (int q = 0; q < 4; ++q)
             if (q == rr) acc = part[q][4 * kb32 + i];
 #pragma unroll
-          for (int j = 0; j < 4; ++j) acc += expf(s[kb32][4 * i + j] - row_max);
+          for (int j = 0; j < 4; ++j) acc += softmax_exp<true>(s[kb32][4 * i + j] - row_max);
 #pragma unroll
           for (int q = 0; q < 4; ++q)
             if (q == rr) part[q][4 * kb32 + i] = acc;
@@ -374,7 +389,8 @@ attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg
     row_sum = (a0 + a2) + (a1 + a3);
   }
 
-  // ============= sweep C: p = bf16(expf(s - max) / sum), context += P V =============
+  // ================== sweep C: p = bf16(softmax), context += P V ==================
+  const float inv_sum = 1.0f / row_sum;  // block-order epilogue multiplies by it
   f32x16 o[2];
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
@@ -391,7 +407,8 @@ attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg
     for (int kb32 = 0; kb32 < 2; ++kb32) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float p = expf(s[kb32][r] - row_max) / row_sum;
+        const float e = softmax_exp<BLOCK_ORDER>(s[kb32][r] - row_max);
+        const float p = BLOCK_ORDER ? e * inv_sum : e / row_sum;
         pf[kb32 * 2 + (r >> 3)][r & 7] = static_cast<__bf16>(p);
       }
     }

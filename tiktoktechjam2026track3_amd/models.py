@@ -62,7 +62,12 @@ def _attention_core(
 ) -> torch.Tensor:
     """Reference score/softmax/PV math for query rows [row_start, row_stop)."""
     seq_len = k.shape[-2]
-    scores = torch.matmul(q[..., row_start:row_stop, :], k.transpose(-2, -1)) * scale
+    k_t = k.transpose(-2, -1)
+    if k_t.is_cuda:
+        # bf16 batched products with a transposed right operand are avoided on
+        # the GPU; the contiguous copy holds the same values
+        k_t = k_t.contiguous()
+    scores = torch.matmul(q[..., row_start:row_stop, :], k_t) * scale
     if causal:
         rows = torch.arange(row_start, row_stop, device=q.device)[:, None]
         cols = torch.arange(seq_len, device=q.device)[None, :]
