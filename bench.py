@@ -1,0 +1,320 @@
+#!/usr/bin/env python3
+"""Encoder-forward benchmark on one MI355X; prints one JSON line.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2]
+
+A step is one forward of ``UserOptimizedTransformer`` (the drop-in candidate
+of transformer_benchmark/models.py:922-1239) over one batch of synthetic input
+already resident in HBM.  The default workload is BASELINE configuration c2
+(B=1, S=128, D=512, H=8, FFN=2048, L=6, bf16, non-causal, weights seeded with
+1, timing input seeded with 1 + 100000 as in timing.py:123); ``--config``
+selects c3, c4 or c5 for the other measurements.
+
+Reported beside the throughput:
+  * ``roofline``: the kernel with the largest share of the forward's time.
+    Each kernel's launches, with the inputs a forward driven launch by launch
+    through the C ABI gives them (the sequence enc_encoder_forward_bf16
+    issues), are timed back to back between hipEvents on the stream they run
+    on (torch's current stream); achieved = algorithmic FLOPs (or bytes) per
+    launch / mean launch duration, against the MI355X dense bf16 MFMA peak
+    (2.5 PFLOP/s) or HBM peak (8 TB/s);
+  * ``cpu_baseline``: the oracle's restatement of the reference forward
+    (oracle/encoder_oracle.py) timed on the host CPU for a bounded sample.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+METRIC = "fwd latency ms + tokens/s + % bf16 MFMA peak per encoder config, 1 GPU"
+MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
+HBM_PEAK_GBS = 8000.0
+
+
+def parse_args(argv=None):
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--config", default="c2", choices=["c2", "c3", "c4", "c5"])
+    p.add_argument("--kernel-reps", type=int, default=10,
+                   help="rounds over the layers' launches when timing each kernel")
+    p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    return p.parse_args(argv)
+
+
+# --------------------------------------------------------------- kernels ----
+
+def profiled_forward(cfg, model, x, mask, native, torch, record):
+    """The native forward's launch sequence (enc_encoder_forward_bf16 issues the
+    same kernels in the same order) driven launch by launch through the C ABI,
+    with ``record(name, work, bound, fn)`` wrapping every launch."""
+    b, s, d = cfg.batch_size, cfg.seq_len, cfg.d_model
+    h, f, hd = cfg.num_heads, cfg.ffn_dim, cfg.d_model // cfg.num_heads
+    t = b * s
+    kv_len = row_mask = None
+    if mask is not None and not bool(mask.all()):
+        kv_len = native.mask_lengths(mask)
+        row_mask = mask.reshape(-1)
+    if cfg.causal:
+        attn_flops = 4.0 * b * d * s * (s + 1) / 2  # causal-live, padding not subtracted
+    else:
+        attn_flops = 4.0 * b * d * s * s
+    ln_bytes = 4.0 * t * d + 4.0 * d
+    xa = x.reshape(t, d)
+    for layer in model.layers:
+        attn = layer.attention
+        xn = record("layernorm", ln_bytes, "hbm",
+                    lambda: native.layernorm(xa, layer.norm1.weight, layer.norm1.bias, layer.norm1.eps))
+        q, k, v_t = record("qkv_proj", 2.0 * t * 3 * d * d, "mfma",
+                           lambda: native.qkv_proj(xn.view(b, s, d), attn.qkv_proj.weight,
+                                                   attn.qkv_proj.bias, h))
+        ctx = record("attention", attn_flops, "mfma",
+                     lambda: native.attention(q, k, v_t, hd**-0.5, cfg.causal, kv_len=kv_len))
+        xb = record("out_proj_residual", 2.0 * t * d * d, "mfma",
+                    lambda: native.linear(ctx.view(t, d), attn.out_proj.weight, attn.out_proj.bias,
+                                          native.ENC_EPI_BIAS_RESIDUAL_KEEP, residual=xa,
+                                          row_mask=row_mask))
+        xn2 = record("layernorm", ln_bytes, "hbm",
+                     lambda: native.layernorm(xb, layer.norm2.weight, layer.norm2.bias, layer.norm2.eps))
+        hid = record("ffn_in_gelu", 2.0 * t * f * d, "mfma",
+                     lambda: native.linear(xn2, layer.ffn_in.weight, layer.ffn_in.bias,
+                                           native.ENC_EPI_BIAS_GELU))
+        xa = record("ffn_out_residual", 2.0 * t * d * f, "mfma",
+                    lambda: native.linear(hid, layer.ffn_out.weight, layer.ffn_out.bias,
+                                          native.ENC_EPI_BIAS_RESIDUAL_ZERO, residual=xb,
+                                          row_mask=row_mask))
+    fn = model.final_norm
+    return record("layernorm", ln_bytes, "hbm",
+                  lambda: native.layernorm(xa, fn.weight, fn.bias, fn.eps, row_mask=row_mask)).view(b, s, d)
+
+
+def kernel_profile(cfg, model, x, mask, native, torch, reps):
+    """Mean launch duration of each kernel of the forward.
+
+    One launch-by-launch forward keeps, per kernel, the launch closures of all
+    layers with their real inputs.  Each kernel is then timed alone: the GPU
+    gets a busy-wait first, so ``reps`` rounds over the layers' launches queue
+    up behind it and run back to back between one pair of hipEvents on the
+    current stream; the duration is the elapsed time over the launch count
+    (inter-launch gaps included, so it slightly overstates the kernel)."""
+    launches = {}
+
+    def record(name, work, bound, fn):
+        entry = launches.setdefault(name, {"work": work, "bound": bound, "fns": []})
+        entry["fns"].append(fn)
+        return fn()
+
+    out = profiled_forward(cfg, model, x, mask, native, torch, record)
+    torch.cuda.synchronize()
+    stats = {}
+    per_step = {name: len(v["fns"]) for name, v in launches.items()}
+    for name, entry in launches.items():
+        fns = entry["fns"]
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        try:
+            torch.cuda._sleep(20_000_000)
+        except Exception:  # the busy-wait only keeps host latency out of the pair
+            pass
+        start.record()
+        for _ in range(reps):
+            for fn in fns:
+                fn()
+        end.record()
+        torch.cuda.synchronize()
+        stats[name] = {"work": entry["work"], "bound": entry["bound"], "per_step": per_step[name],
+                       "mean_ms": start.elapsed_time(end) / (reps * len(fns)),
+                       "launches": reps * len(fns)}
+    return stats, out
+
+
+def load_traffic(kernel, workload):
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE and
+    WRITE_SIZE runs, scaled by the copy-kernel calibration) if recorded."""
+    path = ROOT / "profiles" / "traffic.json"
+    try:
+        table = json.loads(path.read_text())
+    except (OSError, ValueError):
+        return None
+    entry = table.get(f"{kernel}@{workload}")
+    return None if entry is None else entry.get("bytes_per_launch")
+
+
+# ----------------------------------------------------------- CPU baseline ----
+
+def cpu_baseline(spec, baseline_sd, budget_s, torch):
+    """Oracle forward on the host CPU at the config's dtype for about budget_s
+    seconds.  c3/c4 time one sequence (sequences are independent, so tokens/s
+    carries over); c5's score rows do not fit a CPU and are not run."""
+    from oracle.encoder_oracle import encoder_forward, generate_case
+
+    cfg = spec.config
+    if spec.name == "c5":
+        return {"value": None, "unit": "tokens/s", "cores": 0, "kind": "port",
+                "sample": "not run: one c5 sequence is about 85 TFLOP of CPU work "
+                          "(4*D*S^2 = 41 TFLOP of attention per layer, 2 layers), hours on the host"}
+    batch = cfg.batch_size if spec.name == "c2" else 1
+    sd = {k: v.to(torch.bfloat16) for k, v in baseline_sd.items()}
+    x, mask = generate_case(batch, cfg.seq_len, cfg.d_model, torch.device("cpu"), torch.bfloat16,
+                            spec.seed + 100000, spec.padding_ratio)
+    m = None if bool(mask.all()) else mask
+    runs = 0
+    t0 = time.perf_counter()
+    with torch.inference_mode():
+        while True:
+            encoder_forward(sd, x, m, cfg.causal, cfg.num_heads, cfg.num_layers)
+            runs += 1
+            if time.perf_counter() - t0 >= budget_s:
+                break
+    elapsed = time.perf_counter() - t0
+    return {
+        "value": runs * batch * cfg.seq_len / elapsed,
+        "unit": "tokens/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"{runs} forward(s) of {spec.name} with batch {batch} (of {cfg.batch_size}), "
+                  f"bf16, oracle restatement on torch CPU ops, {elapsed:.1f} s",
+    }
+
+
+# ------------------------------------------------------------------ main ----
+
+def main(argv=None) -> int:
+    args = parse_args(argv)
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
+              "(the encoder would shard over the batch across GPUs, which this build "
+              "does not run)", file=sys.stderr)
+        return 2
+
+    sys.path.insert(0, str(ROOT))
+    from tiktoktechjam2026track3_amd.runtime_environment import configure_pre_torch_environment
+
+    configure_pre_torch_environment()
+    import torch
+
+    from tiktoktechjam2026track3_amd import native
+    from tiktoktechjam2026track3_amd.cases import ENCODER_CONFIGS, generate_random_case
+    from tiktoktechjam2026track3_amd.models import (
+        BaselineTransformer, UserOptimizedTransformer, copy_model_weights,
+    )
+
+    if not torch.cuda.is_available():
+        print("bench.py needs an MI355X (no GPU visible)", file=sys.stderr)
+        return 3
+    native.load_library()  # fails loudly if the HIP library is missing
+    spec = ENCODER_CONFIGS[args.config]
+    cfg = spec.config
+    device = torch.device("cuda:0")
+
+    torch.manual_seed(spec.seed)
+    baseline = BaselineTransformer(cfg)
+    candidate = UserOptimizedTransformer(cfg)
+    copy_model_weights(baseline, candidate)
+    baseline_sd = {k: v.detach().clone() for k, v in baseline.state_dict().items()}
+    del baseline
+    candidate = candidate.to(device=device, dtype=torch.bfloat16).eval()
+
+    x, mask = generate_random_case(cfg, device, torch.bfloat16, spec.seed + 100000, spec.padding_ratio, 1.0)
+    tokens = cfg.batch_size * cfg.seq_len
+
+    import contextlib
+
+    # the model's one-line capture notice goes to stderr: stdout carries only the JSON line
+    with torch.inference_mode(), contextlib.redirect_stdout(sys.stderr):
+        for _ in range(args.warmup):
+            candidate(x, mask)
+        torch.cuda.synchronize()
+        pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                 for _ in range(args.steps)]
+        torch.cuda.synchronize()
+        for start, end in pairs:
+            start.record()
+            candidate(x, mask)
+            end.record()
+        torch.cuda.synchronize()
+        total_ms = pairs[0][0].elapsed_time(pairs[-1][1])
+        per_call = [a.elapsed_time(b) for a, b in pairs]
+
+        graph_out = candidate(x, mask)
+        stats, prof_out = kernel_profile(cfg, candidate, x, mask, native, torch, args.kernel_reps)
+        if not torch.equal(prof_out, graph_out):
+            print("warning: launch-by-launch forward differs from the model forward", file=sys.stderr)
+    timed = []
+    for name, v in stats.items():
+        timed.append((v["per_step"] * v["mean_ms"], name, v["per_step"], v["mean_ms"], v["launches"],
+                      v["work"], v["bound"]))
+    timed.sort(reverse=True)
+
+    ms_per_step = total_ms / args.steps
+    median_ms = statistics.median(per_call)
+    d, f, s, b = cfg.d_model, cfg.ffn_dim, cfg.seq_len, cfg.batch_size
+    attn = 4.0 * b * d * s * (s + 1) / 2 if cfg.causal else 4.0 * b * d * s * s
+    flops = cfg.num_layers * (8.0 * tokens * d * d + 4.0 * tokens * d * f + attn)
+
+    _, kname, kcount, kmean, ktimed, kwork, kbound = timed[0]
+    achieved = kwork / (kmean * 1e-3) / (1e12 if kbound == "mfma" else 1e9)
+    peak = MFMA_PEAK_TFLOPS if kbound == "mfma" else HBM_PEAK_GBS
+    roofline = {
+        "bound": kbound,
+        "achieved": round(achieved, 3),
+        "peak": peak,
+        "unit": "TFLOP/s" if kbound == "mfma" else "GB/s",
+        "frac": round(achieved / peak, 5),
+        "traffic": load_traffic(kname, spec.name),
+        "kernel": kname,
+        "launch_ms_mean": round(kmean, 5),
+        "launches_per_step": kcount,
+        "launches_timed": ktimed,
+        "work_per_launch": kwork,
+    }
+    breakdown = {name: {"mean_ms": round(mean, 5), "per_step": count,
+                        "share_est": round(share / ms_per_step, 4)}
+                 for share, name, count, mean, _, _, _ in timed}
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(spec, baseline_sd, args.cpu_seconds, torch)
+
+    line = {
+        "metric": METRIC,
+        "value": tokens * args.steps / (total_ms / 1e3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: x ~ N(0,1) seeded, default-init weights seeded (no checkpoints)",
+        "config": {
+            "workload": spec.name,
+            "batch": b, "seq_len": s, "d_model": d, "num_heads": cfg.num_heads,
+            "ffn_dim": f, "num_layers": cfg.num_layers, "causal": cfg.causal,
+            "padding_ratio": spec.padding_ratio, "parallelism": "single GPU",
+        },
+        "latency_ms_median": median_ms,
+        "pct_bf16_mfma_peak": 100.0 * flops / (median_ms * 1e-3) / (MFMA_PEAK_TFLOPS * 1e12),
+        "flops_per_forward": flops,
+        "roofline": roofline,
+        "kernels": breakdown,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -281,9 +281,10 @@ struct TileShape {
   float efficiency;   // relative MFMA efficiency of the tile shape
 };
 
+// 256x256 is not offered: with 4 wavefronts its 128x128 wave tiles need more
+// than the 512 registers a lane has and spill.
 constexpr TileShape kTiles[] = {
-    {256, 256, 1, 1.00f},
-    {256, 128, 1, 0.90f},
+    {256, 128, 1, 0.85f},
     {128, 128, 2, 0.80f},
     {128, 64, 2, 0.62f},
     {64, 64, 4, 0.45f},
@@ -370,8 +371,9 @@ void gemm_pick_tile(int64_t M, int64_t N, int epilogue, int num_cus, int* bm, in
     const int64_t tiles = ((M + t.bm - 1) / t.bm) * (N / t.bn);
     const int64_t slots = static_cast<int64_t>(num_cus) * t.blocks_per_cu;
     const int64_t rounds = (tiles + slots - 1) / slots;
-    // time ~ rounds * (work of one tile) / (efficiency * concurrent tiles per CU)
-    const double cost = static_cast<double>(rounds) * t.bm * t.bn / (t.efficiency * t.blocks_per_cu);
+    // A round runs blocks_per_cu tiles side by side on every CU, sharing its
+    // MFMA pipes: time ~ rounds * blocks_per_cu * (tile work) / efficiency.
+    const double cost = static_cast<double>(rounds) * t.blocks_per_cu * t.bm * t.bn / t.efficiency;
     if (cost < best * 0.999) {
       best = cost;
       *bm = t.bm;
@@ -396,7 +398,6 @@ hipError_t gemm_bf16(const bf16_t* A, const bf16_t* W, int64_t M, int64_t N, int
   if (split == 2 && chunk == 128) return launch_split<2, 128>(A, W, m, n, k, epi, ep, stream);
   int bm, bn;
   gemm_pick_tile(M, N, epi, num_cus, &bm, &bn);
-  if (bm == 256 && bn == 256) return launch_tile<256, 256>(A, W, m, n, k, epi, ep, stream);
   if (bm == 256 && bn == 128) return launch_tile<256, 128>(A, W, m, n, k, epi, ep, stream);
   if (bm == 128 && bn == 128) return launch_tile<128, 128>(A, W, m, n, k, epi, ep, stream);
   if (bm == 128 && bn == 64) return launch_tile<128, 64>(A, W, m, n, k, epi, ep, stream);
