@@ -76,6 +76,69 @@ __device__ __forceinline__ void store_row_major(const GemmEpilogueArgs& ep, int 
   }
 }
 
+// Writes one 32x32 fp32 accumulator block (rows row0.., cols col0..) through
+// the epilogue.  Lane l holds column col0 + l%32, rows 8*(r/4) + 4*(l/32) + r%4.
+template <int EPI>
+__device__ __forceinline__ void store_block(const GemmEpilogueArgs& ep, int M, int N, int row0,
+                                            int col0, const f32x16& acc) {
+  const int lane = threadIdx.x % kWave;
+  const int l32 = lane & 31;
+  const int lhi = lane >> 5;
+  const int col = col0 + l32;
+  const float bias = bf16_to_f32(ep.bias[col]);
+  if constexpr (EPI == kEpiQkvHeadMajor) {
+    const int D = ep.d_model;
+    const int hd = ep.head_dim;
+    const int which = col / D;
+    const int rem = col - which * D;
+    const int h = rem / hd;
+    const int d = rem - h * hd;
+    const int S = ep.seq_len;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int r0 = row0 + 8 * g + 4 * lhi;  // 4 consecutive rows
+      float y[4];
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) y[jj] = acc[4 * g + jj] + bias;
+      if (which < 2) {
+        bf16_t* dst = which == 0 ? ep.q : ep.k;
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const int row = r0 + jj;
+          if (row < M) {
+            const int b = row / S;
+            const int s = row - b * S;
+            dst[((static_cast<int64_t>(b) * ep.num_heads + h) * S + s) * hd + d] = f32_to_bf16(y[jj]);
+          }
+        }
+      } else {
+        const int b0 = r0 / S;
+        const int s0 = r0 - b0 * S;
+        if (r0 + 3 < M && s0 + 3 < S && (ep.ld_vt & 3) == 0 && (s0 & 3) == 0) {
+          bf16_t* dst = ep.v_t + ((static_cast<int64_t>(b0) * ep.num_heads + h) * hd + d) * ep.ld_vt + s0;
+          *reinterpret_cast<u32x2*>(dst) = u32x2{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
+        } else {
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+            const int row = r0 + jj;
+            if (row < M) {
+              const int b = row / S;
+              const int s = row - b * S;
+              ep.v_t[((static_cast<int64_t>(b) * ep.num_heads + h) * hd + d) * ep.ld_vt + s] = f32_to_bf16(y[jj]);
+            }
+          }
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = row0 + 8 * (r >> 2) + 4 * lhi + (r & 3);
+      if (row < M) store_row_major<EPI>(ep, N, row, col, acc[r], bias);
+    }
+  }
+}
+
 // SPLIT > 1 reproduces the K-split reduction order hipBLASLt picks for some
 // small-M shapes: the K range is cut into CW-wide chunks, chunk c is accumulated
 // into partial (c % SPLIT) in ascending order, and the partials are added
@@ -212,63 +275,291 @@ gemm_bf16_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int
   const int col_base = n0 + wn * (BN / 2);
 #pragma unroll
   for (int j = 0; j < RN; ++j) {
-    const int col = col_base + j * 32 + l32;
-    const float bias = bf16_to_f32(ep.bias[col]);
-    if constexpr (EPI == kEpiQkvHeadMajor) {
-      const int D = ep.d_model;
-      const int hd = ep.head_dim;
-      const int which = col / D;
-      const int rem = col - which * D;
-      const int h = rem / hd;
-      const int d = rem - h * hd;
-      const int S = ep.seq_len;
 #pragma unroll
-      for (int i = 0; i < RM; ++i) {
+    for (int i = 0; i < RM; ++i)
+      store_block<EPI>(ep, M, N, row_base + i * 32, col_base + j * 32, acc[0][i][j]);
+  }
+}
+
+
+// ---------------------------------------------------------------------------
+// Large-tile kernel: BM x BN output tile (256x256, 256x128 or 128x128), four
+// wavefronts in a 2 x 2 grid, each owning a (BM/2) x (BN/2) sub-tile of 32x32
+// fp32 accumulator blocks (up to 256 registers per lane, held in AGPRs).
+//
+// Operands move global -> LDS with global_load_lds_dwordx4, without register
+// staging: one instruction writes 64 consecutive 16-byte LDS chunks, one per
+// lane, so the LDS layout is chosen on the global side.  An LDS row holds one
+// A or W row of the BK-wide K slice as BK/8 chunks of 8 bf16, chunk c stored
+// in slot c ^ swz(row) (swz = row & 7 for 8 chunks a row, (row >> 1) & 3 for
+// 4), so the 32 rows one MFMA fragment read touches at one K chunk land in
+// distinct bank groups.  NS LDS stages form a ring: the loads of K block
+// k + NS - 1 are issued while block k is multiplied, and each iteration waits
+// only for block k + 1 (s_waitcnt vmcnt with the later blocks' loads still
+// outstanding).  The fragments of the next 16-wide K step are read while the
+// current step's MFMAs run.
+//
+// Epilogue: y = bf16(acc + bias) (the nn.Linear output) is staged in LDS as a
+// row-major [BM][BN+8] bf16 tile, then every thread finishes 8 consecutive
+// outputs of one row (GELU / residual / row mask), so the residual reads and
+// the output writes are 16-byte coalesced; the QKV epilogue writes Q and K
+// rows of 8 head channels and V^T columns of 8 sequence positions.
+constexpr int kLdsLimitBytes = 160 * 1024;
+
+// s_waitcnt immediate that waits until at most n vector-memory operations are
+// outstanding (expcnt and lgkmcnt left at their no-wait maxima; gfx9 layout).
+constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+template <int BM, int BN, int BK, int NS>
+struct BigTile {
+  static constexpr int kRM = BM / 64;                       // 32x32 blocks per wave along M
+  static constexpr int kRN = BN / 64;                       // ... along N
+  static constexpr int kStage = (BM + BN) * BK;             // bf16 elements per LDS stage
+  static constexpr int kChunks = BK / 8;                    // 16-byte chunks per LDS row
+  static constexpr int kRowsPerLoad = kWave / kChunks;      // rows one load instruction fills
+  static constexpr int kLoadsA = BM / (4 * kRowsPerLoad);   // per thread per stage
+  static constexpr int kLoadsB = BN / (4 * kRowsPerLoad);
+  static constexpr int kLoads = kLoadsA + kLoadsB;
+  static constexpr int kLdc = BN + 8;                       // epilogue tile row stride
+  static constexpr int kSmem = (NS * kStage > BM * kLdc) ? NS * kStage : BM * kLdc;
+  static_assert(BK == 32 || BK == 64, "BK");
+  static_assert(kSmem * 2 <= kLdsLimitBytes, "LDS budget");
+  static_assert(NS >= 2 && kLoads * (NS - 2) < 64, "vmcnt range");
+  __device__ static constexpr int swz(int row) { return kChunks == 8 ? (row & 7) : ((row >> 1) & 3); }
+};
+
+template <int EPI>
+__device__ __forceinline__ void finish8(const GemmEpilogueArgs& ep, int N, int row, int col,
+                                        const float (&y)[8]) {
+  const int64_t idx = static_cast<int64_t>(row) * N + col;
+  u32x4 w;
+  if constexpr (EPI == kEpiBias) {
+    w = u32x4{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]), pack_bf16x2(y[4], y[5]), pack_bf16x2(y[6], y[7])};
+  } else if constexpr (EPI == kEpiBiasGelu) {
+    float g[8];
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int row0 = row_base + i * 32 + 8 * g + 4 * lhi;  // 4 consecutive rows
-          float y[4];
+    for (int e = 0; e < 8; ++e) g[e] = gelu_erf(y[e]);
+    w = u32x4{pack_bf16x2(g[0], g[1]), pack_bf16x2(g[2], g[3]), pack_bf16x2(g[4], g[5]), pack_bf16x2(g[6], g[7])};
+  } else {
+    const u32x4 r = *reinterpret_cast<const u32x4*>(ep.residual + idx);
+    bool keep = true;
+    if (ep.row_mask != nullptr) keep = ep.row_mask[row] != 0;
+    if (keep) {
+      float o[8];
 #pragma unroll
-          for (int jj = 0; jj < 4; ++jj) y[jj] = acc[0][i][j][4 * g + jj] + bias;
-          if (which < 2) {
-            bf16_t* dst = which == 0 ? ep.q : ep.k;
-#pragma unroll
-            for (int jj = 0; jj < 4; ++jj) {
-              const int row = row0 + jj;
-              if (row < M) {
-                const int b = row / S;
-                const int s = row - b * S;
-                dst[((static_cast<int64_t>(b) * ep.num_heads + h) * S + s) * hd + d] = f32_to_bf16(y[jj]);
-              }
-            }
-          } else {
-            const int b0 = row0 / S;
-            const int s0 = row0 - b0 * S;
-            if (row0 + 3 < M && s0 + 3 < S && (ep.ld_vt & 3) == 0 && (s0 & 3) == 0) {
-              bf16_t* dst = ep.v_t + ((static_cast<int64_t>(b0) * ep.num_heads + h) * hd + d) * ep.ld_vt + s0;
-              u32x2 w = {pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
-              *reinterpret_cast<u32x2*>(dst) = w;
-            } else {
-#pragma unroll
-              for (int jj = 0; jj < 4; ++jj) {
-                const int row = row0 + jj;
-                if (row < M) {
-                  const int b = row / S;
-                  const int s = row - b * S;
-                  ep.v_t[((static_cast<int64_t>(b) * ep.num_heads + h) * hd + d) * ep.ld_vt + s] = f32_to_bf16(y[jj]);
-                }
-              }
-            }
-          }
-        }
+      for (int e = 0; e < 4; ++e) {
+        o[2 * e] = lo_bf16(r[e]) + y[2 * e];
+        o[2 * e + 1] = hi_bf16(r[e]) + y[2 * e + 1];
       }
+      w = u32x4{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]), pack_bf16x2(o[4], o[5]), pack_bf16x2(o[6], o[7])};
     } else {
+      w = (EPI == kEpiResidualKeep) ? r : u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  *reinterpret_cast<u32x4*>(ep.out + idx) = w;
+}
+
+template <int BM, int BN, int BK, int NS, int EPI, int OCC = 1>
+__global__ void __launch_bounds__(kThreads, OCC)
+gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int M, int N, int K,
+                GemmEpilogueArgs ep) {
+  using T = BigTile<BM, BN, BK, NS>;
+  constexpr int RM = T::kRM, RN = T::kRN;
+  __shared__ __attribute__((aligned(16))) bf16_t smem[T::kSmem];
+
+  const int tiles_m = (M + BM - 1) / BM;
+  const int tiles_n = N / BN;
+  int tm, tn;
+  map_tile(tiles_m, tiles_n, &tm, &tn);
+  const int m0 = tm * BM;
+  const int n0 = tn * BN;
+
+  const int tid = threadIdx.x;
+  const int lane = tid % kWave;
+  const int wave = tid / kWave;
+  const int wm = wave >> 1;
+  const int wn = wave & 1;
+  const int l32 = lane & 31;
+  const int lhi = lane >> 5;
+
+  // Load instruction j of wavefront w fills LDS rows R (4 j + w) .. + R - 1
+  // (R = rows per instruction); lane -> row + lane / chunks, slot lane % chunks,
+  // holding global chunk slot ^ swz(row).  Offsets are relative to the tile's
+  // first row (32-bit); the bases are uniform.
+  const int lrow = lane / T::kChunks;
+  const int gcol = ((lane % T::kChunks) ^ T::swz(lrow)) * 8;
+  const bf16_t* a_tile = A + static_cast<int64_t>(m0) * K;
+  const bf16_t* w_tile = W + static_cast<int64_t>(n0) * K;
+  const int a_rows_left = M - 1 - m0;  // rows past M re-load the last row, never stored
+  auto issue_loads = [&](int stage, int k0) {
+    bf16_t* sa = smem + stage * T::kStage;
+    bf16_t* sb = sa + BM * BK;
 #pragma unroll
-      for (int i = 0; i < RM; ++i) {
+    for (int j = 0; j < T::kLoadsA; ++j) {
+      const int row = T::kRowsPerLoad * (4 * j + wave);
+      const int ra = min(row + lrow, a_rows_left);
+      __builtin_amdgcn_global_load_lds(a_tile + k0 + (ra * K + gcol), sa + row * BK, 16, 0, 0);
+    }
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = row_base + i * 32 + 8 * (r >> 2) + 4 * lhi + (r & 3);
-          if (row < M) store_row_major<EPI>(ep, N, row, col, acc[0][i][j][r], bias);
+    for (int j = 0; j < T::kLoadsB; ++j) {
+      const int row = T::kRowsPerLoad * (4 * j + wave);
+      __builtin_amdgcn_global_load_lds(w_tile + k0 + ((row + lrow) * K + gcol), sb + row * BK, 16, 0, 0);
+    }
+  };
+
+  f32x16 acc[RM][RN];
+#pragma unroll
+  for (int i = 0; i < RM; ++i)
+#pragma unroll
+    for (int j = 0; j < RN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  // Fragment rows: A row wm*(BM/2) + 32 i + l32, W row wn*(BN/2) + 32 j + l32;
+  // the row's low bits are l32's, so the swizzle is per lane.
+  const int a_off = (wm * (BM / 2) + l32) * BK;
+  const int b_off = BM * BK + (wn * (BN / 2) + l32) * BK;
+  const int swz = T::swz(l32);
+  auto read_frags = [&](int stage, int ks, bf16x8 (&af)[RM], bf16x8 (&bf)[RN]) {
+    const bf16_t* st = smem + stage * T::kStage;
+    const int slot = ((2 * ks + lhi) ^ swz) * 8;
+#pragma unroll
+    for (int i = 0; i < RM; ++i) af[i] = *reinterpret_cast<const bf16x8*>(st + a_off + i * 32 * BK + slot);
+#pragma unroll
+    for (int j = 0; j < RN; ++j) bf[j] = *reinterpret_cast<const bf16x8*>(st + b_off + j * 32 * BK + slot);
+  };
+  // Wait until K block `ready` has landed, given that blocks up to `issued`
+  // were requested (each block is T::kLoads instructions of this thread).
+  auto wait_block = [&](int ready, int issued) {
+    const int later = min(issued - ready, NS - 2);
+    if (later <= 0) {
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    } else if (later == 1) {
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(T::kLoads));
+    } else {
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(T::kLoads * (NS - 2 > 1 ? 2 : 1)));
+    }
+  };
+  static_assert(NS <= 4, "wait_block covers at most two later blocks");
+
+  const int KT = K / BK;
+  int issued = -1;
+  for (int p = 0; p < NS - 1 && p < KT; ++p) {
+    issue_loads(p, p * BK);
+    issued = p;
+  }
+  wait_block(0, issued);
+  __syncthreads();
+  bf16x8 af[RM], bf[RN];
+  read_frags(0, 0, af, bf);
+  int stage = 0;
+  for (int kt = 0; kt < KT; ++kt) {
+    if (kt + NS - 1 < KT) {
+      int ls = stage + NS - 1;
+      if (ls >= NS) ls -= NS;
+      issue_loads(ls, (kt + NS - 1) * BK);
+      issued = kt + NS - 1;
+    }
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      bf16x8 an[RM], bn[RN];
+      if (ks + 1 < BK / 16) read_frags(stage, ks + 1, an, bn);
+#pragma unroll
+      for (int i = 0; i < RM; ++i)
+#pragma unroll
+        for (int j = 0; j < RN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
+      if (ks + 1 < BK / 16) {
+#pragma unroll
+        for (int i = 0; i < RM; ++i) af[i] = an[i];
+#pragma unroll
+        for (int j = 0; j < RN; ++j) bf[j] = bn[j];
+      }
+    }
+    // block kt + 1 landed for every wave; nobody reads `stage` any more
+    if (kt + 1 < KT) wait_block(kt + 1, issued);
+    __syncthreads();
+    stage = stage + 1 == NS ? 0 : stage + 1;
+    if (kt + 1 < KT) read_frags(stage, 0, af, bf);
+  }
+
+  // ---- epilogue: y = bf16(acc + bias) into LDS, then 8 outputs per thread ----
+  bf16_t* sc = smem;  // every wave passed the last barrier: the stages are free
+#pragma unroll
+  for (int j = 0; j < RN; ++j) {
+    const int cl = wn * (BN / 2) + j * 32 + l32;
+    const float bias = bf16_to_f32(ep.bias[n0 + cl]);
+#pragma unroll
+    for (int i = 0; i < RM; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int rl = wm * (BM / 2) + i * 32 + 8 * (r >> 2) + 4 * lhi + (r & 3);
+        sc[rl * T::kLdc + cl] = f32_to_bf16(acc[i][j][r] + bias);
+      }
+    }
+  }
+  __syncthreads();
+
+  if constexpr (EPI != kEpiQkvHeadMajor) {
+    constexpr int kPerRow = BN / 8;
+    constexpr int kRowsPerPass = kThreads / kPerRow;
+    const int c8 = (tid % kPerRow) * 8;
+    for (int rl = tid / kPerRow; rl < BM; rl += kRowsPerPass) {
+      const int row = m0 + rl;
+      if (row >= M) break;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(sc + rl * T::kLdc + c8);
+      const float y[8] = {lo_bf16(v[0]), hi_bf16(v[0]), lo_bf16(v[1]), hi_bf16(v[1]),
+                          lo_bf16(v[2]), hi_bf16(v[2]), lo_bf16(v[3]), hi_bf16(v[3])};
+      finish8<EPI>(ep, N, row, n0 + c8, y);
+    }
+  } else {
+    const int D = ep.d_model;
+    const int hd = ep.head_dim;
+    const int S = ep.seq_len;
+    // Q / K: 8 consecutive channels of one head, one row
+    constexpr int kPerRow = BN / 8;
+    const int c8 = (tid % kPerRow) * 8;
+    const int col = n0 + c8;
+    const int which = col / D;
+    if (which < 2) {
+      const int h = (col - which * D) / hd;
+      const int d = (col - which * D) - h * hd;
+      bf16_t* dst = which == 0 ? ep.q : ep.k;
+      for (int rl = tid / kPerRow; rl < BM; rl += kThreads / kPerRow) {
+        const int row = m0 + rl;
+        if (row >= M) break;
+        const int b = row / S;
+        const int s = row - b * S;
+        *reinterpret_cast<u32x4*>(dst + ((static_cast<int64_t>(b) * ep.num_heads + h) * S + s) * hd + d) =
+            *reinterpret_cast<const u32x4*>(sc + rl * T::kLdc + c8);
+      }
+    }
+    // V^T: one channel, 8 consecutive rows (sequence positions)
+    for (int item = tid; item < BN * (BM / 8); item += kThreads) {
+      const int cl = item % BN;
+      const int r8 = (item / BN) * 8;
+      const int vcol = n0 + cl;
+      if (vcol / D != 2) continue;
+      const int h = (vcol - 2 * D) / hd;
+      const int d = (vcol - 2 * D) - h * hd;
+      const int row0 = m0 + r8;
+      if (row0 >= M) continue;
+      const int b0 = row0 / S;
+      const int s0 = row0 - b0 * S;
+      bf16_t* dst = ep.v_t + ((static_cast<int64_t>(b0) * ep.num_heads + h) * hd + d) * ep.ld_vt + s0;
+      if (row0 + 7 < M && s0 + 7 < S && (s0 & 7) == 0 && (ep.ld_vt & 7) == 0) {
+        uint32_t p[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          p[e] = static_cast<uint32_t>(sc[(r8 + 2 * e) * T::kLdc + cl]) |
+                 (static_cast<uint32_t>(sc[(r8 + 2 * e + 1) * T::kLdc + cl]) << 16);
+        *reinterpret_cast<u32x4*>(dst) = u32x4{p[0], p[1], p[2], p[3]};
+      } else {
+        for (int e = 0; e < 8 && row0 + e < M; ++e) {
+          const int row = row0 + e;
+          const int b = row / S;
+          const int s = row - b * S;
+          ep.v_t[((static_cast<int64_t>(b) * ep.num_heads + h) * hd + d) * ep.ld_vt + s] = sc[(r8 + e) * T::kLdc + cl];
         }
       }
     }
@@ -330,6 +621,42 @@ hipError_t launch_split(const bf16_t* A, const bf16_t* W, int M, int N, int K, i
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+template <int BM, int BN, int BK, int NS, int OCC = 1>
+hipError_t launch_big(const bf16_t* A, const bf16_t* W, int M, int N, int K, int epi,
+                      const GemmEpilogueArgs& ep, hipStream_t st) {
+  const int tiles = ((M + BM - 1) / BM) * (N / BN);
+  const dim3 grid(tiles), block(kThreads);
+  switch (epi) {
+    case kEpiBias: hipLaunchKernelGGL((gemm_big_kernel<BM, BN, BK, NS, kEpiBias, OCC>), grid, block, 0, st, A, W, M, N, K, ep); break;
+    case kEpiBiasGelu: hipLaunchKernelGGL((gemm_big_kernel<BM, BN, BK, NS, kEpiBiasGelu, OCC>), grid, block, 0, st, A, W, M, N, K, ep); break;
+    case kEpiResidualKeep: hipLaunchKernelGGL((gemm_big_kernel<BM, BN, BK, NS, kEpiResidualKeep, OCC>), grid, block, 0, st, A, W, M, N, K, ep); break;
+    case kEpiResidualZero: hipLaunchKernelGGL((gemm_big_kernel<BM, BN, BK, NS, kEpiResidualZero, OCC>), grid, block, 0, st, A, W, M, N, K, ep); break;
+    case kEpiQkvHeadMajor: hipLaunchKernelGGL((gemm_big_kernel<BM, BN, BK, NS, kEpiQkvHeadMajor, OCC>), grid, block, 0, st, A, W, M, N, K, ep); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+// Tile of the large-tile kernel for this shape, or 0 when the small-tile
+// kernel should run: the operands must be 16-byte aligned (16-byte loads per
+// lane), the residual / outputs too (16-byte epilogue stores), and the tile
+// count should fill the 256 CUs.
+int pick_big_tile(int64_t M, int64_t N, const bf16_t* A, const bf16_t* W, const GemmEpilogueArgs& ep,
+                  bool ep_is_gelu) {
+  auto al = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+  if (!al(A) || !al(W) || !al(ep.out) || !al(ep.residual) || !al(ep.q) || !al(ep.k) || !al(ep.v_t)) return 0;
+  if (M < 1024) return 0;
+  // The erf GELU epilogue is long dependent VALU work; with two resident
+  // 256x128 tiles per CU one tile's epilogue overlaps the other's MFMA loop.
+  if (ep_is_gelu && N % 128 == 0) return 256129;
+  const int64_t t256 = ((M + 255) / 256) * (N / 256);
+  if (N % 256 == 0 && t256 >= 256) return 256256;
+  const int64_t t256x128 = ((M + 255) / 256) * (N / 128);
+  if (N % 128 == 0 && t256x128 >= 256) return 256128;
+  if (N % 128 == 0) return 128128;
+  return 0;
 }
 
 }  // namespace
@@ -396,6 +723,13 @@ hipError_t gemm_bf16(const bf16_t* A, const bf16_t* W, int64_t M, int64_t N, int
   if (split == 4 && chunk == 32) return launch_split<4, 32>(A, W, m, n, k, epi, ep, stream);
   if (split == 4 && chunk == 64) return launch_split<4, 64>(A, W, m, n, k, epi, ep, stream);
   if (split == 2 && chunk == 128) return launch_split<2, 128>(A, W, m, n, k, epi, ep, stream);
+  switch (pick_big_tile(M, N, A, W, ep, epi == kEpiBiasGelu)) {
+    case 256129: return launch_big<256, 128, 32, 3, 2>(A, W, m, n, k, epi, ep, stream);
+    case 256256: return launch_big<256, 256, 32, 4>(A, W, m, n, k, epi, ep, stream);
+    case 256128: return launch_big<256, 128, 64, 3>(A, W, m, n, k, epi, ep, stream);
+    case 128128: return launch_big<128, 128, 64, 3>(A, W, m, n, k, epi, ep, stream);
+    default: break;
+  }
   int bm, bn;
   gemm_pick_tile(M, N, epi, num_cus, &bm, &bn);
   if (bm == 256 && bn == 128) return launch_tile<256, 128>(A, W, m, n, k, epi, ep, stream);
