@@ -95,7 +95,8 @@ int enc_qkv_proj_bf16(const void* x, const void* weight, const void* bias,
  *   s_ij = bf16(bf16(q_i . k_j) * scale)
  *   p_ij = bf16(softmax_j(s_ij)) in fp32 ;  context = bf16(sum_j p_ij v_j)
  * bit for bit as the reference computes them with torch on ROCm (the softmax
- * max/sum/divide follow torch's reduction order).  seq_len above 2048 must be
+ * max/sum/divide follow torch's reduction order), by sweeping the keys three
+ * times (row max, row sum, probabilities + P.V).  seq_len above 2048 must be
  * a multiple of 4.
  * Key j is excluded when causal and j > i, when kv_len is non-null and
  * j >= kv_len[b] (prefix padding), or when key_mask is non-null and
@@ -113,11 +114,29 @@ int enc_attention_fwd_bf16(const void* q, const void* k, const void* v_t,
                            int32_t causal, const int32_t* kv_len,
                            const uint8_t* key_mask, void* stream);
 
+/* One-pass attention with an online softmax: same arguments, masking and
+ * layouts as enc_attention_fwd_bf16, any seq_len.  Scores are rounded as the
+ * reference rounds them, but the exponentials exp(s_ij - m_i) are rounded to
+ * bf16 before the division by the row sum instead of after it, so the context
+ * differs from the reference's by bf16 rounding noise of the weights.  That
+ * noise compounds through a deep bf16 stack past the reference's elementwise
+ * gate, so the encoder uses it only when asked (ENC_FWD_ONLINE_ATTENTION).
+ * Same reference code as enc_attention_fwd_bf16 (models.py:55-75). */
+int enc_attention_online_fwd_bf16(const void* q, const void* k, const void* v_t,
+                                  void* context, int64_t batch,
+                                  int64_t num_heads, int64_t seq_len,
+                                  int64_t head_dim, float scale, int32_t causal,
+                                  const int32_t* kv_len,
+                                  const uint8_t* key_mask, void* stream);
+
 /* kv_len[b] = number of valid tokens in mask[b, :] (int32, device).  Equal to
  * the prefix length for the prefix masks built by generate_random_case
  * (transformer_benchmark/cases.py:87-97). */
 int enc_mask_lengths(const uint8_t* mask, int64_t batch, int64_t seq_len,
                      int32_t* kv_len, void* stream);
+
+/* flags of enc_encoder_forward_bf16 */
+#define ENC_FWD_ONLINE_ATTENTION 1 /* one-pass online-softmax attention      */
 
 /* Bytes of device workspace enc_encoder_forward_bf16 needs for this shape. */
 int64_t enc_encoder_workspace_bytes(int64_t batch, int64_t seq_len,
@@ -136,7 +155,7 @@ int64_t enc_encoder_workspace_bytes(int64_t batch, int64_t seq_len,
  * padded rows (models.py:736-737) and so is the final output
  * (models.py:917-918).  kv_len / key_mask are passed to the attention as in
  * enc_attention_fwd_bf16 (at most one of them non-null).  x is not modified;
- * out may not alias x or the workspace.
+ * out may not alias x or the workspace.  flags: 0 or ENC_FWD_ONLINE_ATTENTION.
  * Replaces UserOptimizedTransformer.forward / _forward_eager
  * (transformer_benchmark/models.py:1020-1049, 1202-1239) and the block
  * forward (models.py:772-892). */
@@ -147,7 +166,8 @@ int enc_encoder_forward_bf16(const void* x, void* out, void* workspace,
                              int64_t num_heads, int64_t ffn_dim,
                              int64_t num_layers, float eps, int32_t causal,
                              const int32_t* kv_len, const uint8_t* key_mask,
-                             const uint8_t* row_mask, void* stream);
+                             const uint8_t* row_mask, int32_t flags,
+                             void* stream);
 
 #ifdef __cplusplus
 }

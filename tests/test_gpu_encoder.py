@@ -84,6 +84,24 @@ def test_graph_replay_matches_eager(device):
         assert compare(ref, replayed, RTOL, ATOL)["passed"]
 
 
+def test_online_attention_encoder_stays_close(device):
+    """The opt-in one-pass attention: its bf16 weight-rounding noise compounds
+    over the layers, so it is held to a looser bound than the reference's gate
+    (the exact default is what meets the gate)."""
+    spec = ENCODER_CONFIGS["c3"]
+    cfg = spec.config
+    sd, candidate = build_models(cfg, spec.seed, device)
+    candidate.online_attention = True
+    with torch.inference_mode():
+        x, mask = generate_random_case(cfg, device, torch.bfloat16, spec.seed, spec.padding_ratio, 1.0)
+        out = candidate(x, mask)
+        ref = encoder_forward(sd, x, mask, cfg.causal, cfg.num_heads, cfg.num_layers)
+    result = compare(ref, out, RTOL, ATOL)
+    print(f"[parity] c3 online attention: {result}", flush=True)
+    assert result["max_abs_error"] < 0.25
+    assert result["failed"] < 0.01 * result["total"]
+
+
 def test_unsupported_dtype_raises(device):
     cfg = TransformerConfig(1, 16, 512, 8, 1024, 1, False)
     model = UserOptimizedTransformer(cfg).to(device).eval()

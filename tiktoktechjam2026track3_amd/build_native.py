@@ -22,7 +22,7 @@ LIBRARY_NAME = "libmi355x_encoder.so"
 LIBRARY_PATH = PACKAGE_DIR / LIBRARY_NAME
 OFFLOAD_ARCH = "gfx950"
 
-SOURCES = ("layernorm.hip", "gemm.hip", "attention.hip", "capi.hip")
+SOURCES = ("layernorm.hip", "gemm.hip", "attention.hip", "flash_attention.hip", "capi.hip")
 
 # Packed FP32 VALU ops (v_pk_fma_f32 and friends) are disabled for every device
 # compile; hipcc's host pass prints a harmless "not a recognized feature" note.

@@ -81,7 +81,7 @@ EncoderWorkspace plan_workspace(int64_t B, int64_t S, int64_t D, int64_t H, int6
 
 bool shape_ok(int64_t v) { return v > 0 && v < (int64_t(1) << 31); }
 
-int check_encoder_shape(int64_t B, int64_t S, int64_t D, int64_t H, int64_t F) {
+int check_encoder_shape(int64_t B, int64_t S, int64_t D, int64_t H, int64_t F, bool exact_attention) {
   if (!shape_ok(B) || !shape_ok(S) || !shape_ok(D) || !shape_ok(H) || !shape_ok(F))
     return fail(ENC_ERR_INVALID, "batch, seq_len, d_model, num_heads and ffn_dim must be positive");
   if (D % H != 0) return fail(ENC_ERR_INVALID, "d_model must be divisible by num_heads");
@@ -91,7 +91,7 @@ int check_encoder_shape(int64_t B, int64_t S, int64_t D, int64_t H, int64_t F) {
   if (!enc::layernorm_supported(D))
     return fail(ENC_ERR_UNSUPPORTED, "LayerNorm width must be a power of two in [256, 4096] (got " +
                                          std::to_string(D) + ")");
-  if (!enc::attention_seq_supported(S))
+  if (exact_attention && !enc::attention_seq_supported(S))
     return fail(ENC_ERR_UNSUPPORTED, "seq_len above 2048 must be a multiple of 4 (got " +
                                          std::to_string(S) + ")");
   if (D % 64 != 0 || F % 64 != 0)
@@ -104,7 +104,7 @@ int check_encoder_shape(int64_t B, int64_t S, int64_t D, int64_t H, int64_t F) {
 
 extern "C" {
 
-int enc_version(void) { return (1 << 16) | 0; }
+int enc_version(void) { return (1 << 16) | 1; }
 
 const char* enc_last_error(void) { return g_last_error.c_str(); }
 
@@ -176,9 +176,11 @@ int enc_qkv_proj_bf16(const void* x, const void* weight, const void* bias, void*
   return ok();
 }
 
-int enc_attention_fwd_bf16(const void* q, const void* k, const void* v_t, void* context, int64_t batch,
-                           int64_t num_heads, int64_t seq_len, int64_t head_dim, float scale, int32_t causal,
-                           const int32_t* kv_len, const uint8_t* key_mask, void* stream) {
+namespace {
+
+int attention_entry(bool exact, const void* q, const void* k, const void* v_t, void* context, int64_t batch,
+                    int64_t num_heads, int64_t seq_len, int64_t head_dim, float scale, int32_t causal,
+                    const int32_t* kv_len, const uint8_t* key_mask, void* stream) {
   if (batch < 0 || num_heads <= 0 || seq_len < 0 || head_dim <= 0)
     return fail(ENC_ERR_INVALID, "attention: bad shape");
   if (batch == 0 || seq_len == 0) return ok();
@@ -186,17 +188,34 @@ int enc_attention_fwd_bf16(const void* q, const void* k, const void* v_t, void* 
   if (head_dim != 64) return fail(ENC_ERR_UNSUPPORTED, "attention: head_dim must be 64");
   if (kv_len && key_mask) return fail(ENC_ERR_INVALID, "attention: pass kv_len or key_mask, not both");
   if (!(scale > 0.f)) return fail(ENC_ERR_INVALID, "attention: scale must be positive");
-  if (!enc::attention_seq_supported(seq_len))
+  if (exact && !enc::attention_seq_supported(seq_len))
     return fail(ENC_ERR_UNSUPPORTED, "attention: seq_len above 2048 must be a multiple of 4");
-  if (batch * num_heads * ((seq_len + 127) / 128) >= (int64_t(1) << 31))
+  if (seq_len >= (int64_t(1) << 30) || batch * num_heads * ((seq_len + 31) / 32) >= (int64_t(1) << 31))
     return fail(ENC_ERR_UNSUPPORTED, "attention: grid too large");
-  hipError_t e = enc::attention_fwd_bf16(
-      static_cast<const enc::bf16_t*>(q), static_cast<const enc::bf16_t*>(k), static_cast<const enc::bf16_t*>(v_t),
-      static_cast<enc::bf16_t*>(context), static_cast<int>(batch), static_cast<int>(num_heads),
-      static_cast<int>(seq_len), static_cast<int>(head_dim), scale, causal != 0, kv_len, key_mask,
-      static_cast<hipStream_t>(stream));
+  auto fn = exact ? enc::attention_fwd_bf16 : enc::flash_attention_fwd_bf16;
+  hipError_t e = fn(static_cast<const enc::bf16_t*>(q), static_cast<const enc::bf16_t*>(k),
+                    static_cast<const enc::bf16_t*>(v_t), static_cast<enc::bf16_t*>(context),
+                    static_cast<int>(batch), static_cast<int>(num_heads), static_cast<int>(seq_len),
+                    static_cast<int>(head_dim), scale, causal != 0, kv_len, key_mask,
+                    static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail_hip(e, "attention launch");
   return ok();
+}
+
+}  // namespace
+
+int enc_attention_fwd_bf16(const void* q, const void* k, const void* v_t, void* context, int64_t batch,
+                           int64_t num_heads, int64_t seq_len, int64_t head_dim, float scale, int32_t causal,
+                           const int32_t* kv_len, const uint8_t* key_mask, void* stream) {
+  return attention_entry(true, q, k, v_t, context, batch, num_heads, seq_len, head_dim, scale, causal, kv_len,
+                         key_mask, stream);
+}
+
+int enc_attention_online_fwd_bf16(const void* q, const void* k, const void* v_t, void* context, int64_t batch,
+                                  int64_t num_heads, int64_t seq_len, int64_t head_dim, float scale,
+                                  int32_t causal, const int32_t* kv_len, const uint8_t* key_mask, void* stream) {
+  return attention_entry(false, q, k, v_t, context, batch, num_heads, seq_len, head_dim, scale, causal, kv_len,
+                         key_mask, stream);
 }
 
 int enc_mask_lengths(const uint8_t* mask, int64_t batch, int64_t seq_len, int32_t* kv_len, void* stream) {
@@ -220,8 +239,10 @@ int enc_encoder_forward_bf16(const void* x, void* out, void* workspace, int64_t 
                              const void* const* weights, int64_t batch, int64_t seq_len, int64_t d_model,
                              int64_t num_heads, int64_t ffn_dim, int64_t num_layers, float eps, int32_t causal,
                              const int32_t* kv_len, const uint8_t* key_mask, const uint8_t* row_mask,
-                             void* stream) {
-  int rc = check_encoder_shape(batch, seq_len, d_model, num_heads, ffn_dim);
+                             int32_t flags, void* stream) {
+  if (flags & ~ENC_FWD_ONLINE_ATTENTION) return fail(ENC_ERR_INVALID, "encoder: unknown flags");
+  const bool exact = (flags & ENC_FWD_ONLINE_ATTENTION) == 0;
+  int rc = check_encoder_shape(batch, seq_len, d_model, num_heads, ffn_dim, exact);
   if (rc != ENC_OK) return rc;
   if (num_layers < 0) return fail(ENC_ERR_INVALID, "encoder: num_layers must be >= 0");
   if (!x || !out || !workspace || !weights) return fail(ENC_ERR_INVALID, "encoder: null pointer");
@@ -273,9 +294,9 @@ int enc_encoder_forward_bf16(const void* x, void* out, void* workspace, int64_t 
     e = enc::gemm_bf16(ln, W(layer, 2), T, 3 * D, D, enc::kEpiQkvHeadMajor, qa, cus, st);
     if (e != hipSuccess) return fail_hip(e, "encoder qkv");
     // attention -> context [T, D]
-    e = enc::attention_fwd_bf16(q, k, vt, ctx, static_cast<int>(batch), static_cast<int>(H),
-                                static_cast<int>(seq_len), static_cast<int>(D / H), scale, causal != 0, kv_len,
-                                key_mask, st);
+    auto attention = exact ? enc::attention_fwd_bf16 : enc::flash_attention_fwd_bf16;
+    e = attention(q, k, vt, ctx, static_cast<int>(batch), static_cast<int>(H), static_cast<int>(seq_len),
+                  static_cast<int>(D / H), scale, causal != 0, kv_len, key_mask, st);
     if (e != hipSuccess) return fail_hip(e, "encoder attention");
     // out_proj + residual; padded rows keep the residual (attention output is 0 there)
     enc::GemmEpilogueArgs oa;

@@ -27,6 +27,8 @@ ENC_ERR_UNSUPPORTED = 2
 ENC_ERR_HIP = 3
 ENC_ERR_OOM = 4
 
+ENC_FWD_ONLINE_ATTENTION = 1
+
 ENC_EPI_BIAS = 0
 ENC_EPI_BIAS_GELU = 1
 ENC_EPI_BIAS_RESIDUAL_KEEP = 2
@@ -48,12 +50,17 @@ SIGNATURES = (
         ctypes.c_int,
         (_VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _F32, _I32, _VP, _VP, _VP),
     ),
+    (
+        "enc_attention_online_fwd_bf16",
+        ctypes.c_int,
+        (_VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _F32, _I32, _VP, _VP, _VP),
+    ),
     ("enc_mask_lengths", ctypes.c_int, (_VP, _I64, _I64, _VP, _VP)),
     ("enc_encoder_workspace_bytes", ctypes.c_int64, (_I64, _I64, _I64, _I64, _I64)),
     (
         "enc_encoder_forward_bf16",
         ctypes.c_int,
-        (_VP, _VP, _VP, _I64, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _F32, _I32, _VP, _VP, _VP, _VP),
+        (_VP, _VP, _VP, _I64, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _F32, _I32, _VP, _VP, _VP, _I32, _VP),
     ),
 )
 
@@ -227,8 +234,14 @@ def attention(
     kv_len: Optional[torch.Tensor] = None,
     key_mask: Optional[torch.Tensor] = None,
     out: Optional[torch.Tensor] = None,
+    online: bool = False,
 ) -> torch.Tensor:
-    """Streaming attention; returns context [B, S, H*hd] (enc_attention_fwd_bf16)."""
+    """Streaming attention; returns context [B, S, H*hd].
+
+    By default the three-sweep kernel that forms the reference's bf16
+    probabilities bit for bit (enc_attention_fwd_bf16); ``online=True`` runs
+    the one-pass online-softmax kernel (enc_attention_online_fwd_bf16).
+    """
     for tensor, name in ((q, "q"), (k, "k"), (v_t, "v_t")):
         _require(tensor, name, torch.bfloat16)
     batch, heads, seq_len, hd = q.shape
@@ -244,9 +257,10 @@ def attention(
     if kv_len is not None:
         _require(kv_len, "kv_len", torch.int32)
     mask = None if key_mask is None else key_mask.contiguous().view(torch.uint8)
+    name = "enc_attention_online_fwd_bf16" if online else "enc_attention_fwd_bf16"
     _check(
-        "enc_attention_fwd_bf16",
-        load_library().enc_attention_fwd_bf16(
+        name,
+        getattr(load_library(), name)(
             q.data_ptr(), k.data_ptr(), v_t.data_ptr(), out.data_ptr(), batch, heads, seq_len, hd,
             float(scale), int(bool(causal)), _ptr(kv_len), _ptr(mask), _stream(q.device),
         ),
@@ -290,6 +304,7 @@ def encoder_forward(
     kv_len: Optional[torch.Tensor],
     key_mask: Optional[torch.Tensor],
     row_mask: Optional[torch.Tensor],
+    online_attention: bool = False,
 ) -> None:
     """Run the whole encoder through enc_encoder_forward_bf16.
 
@@ -303,6 +318,7 @@ def encoder_forward(
         load_library().enc_encoder_forward_bf16(
             x.data_ptr(), out.data_ptr(), workspace.data_ptr(), workspace.numel(), table.value,
             batch, seq_len, d_model, num_heads, ffn_dim, num_layers, float(eps), int(bool(causal)),
-            _ptr(kv_len), _ptr(key_mask), _ptr(row_mask), _stream(x.device),
+            _ptr(kv_len), _ptr(key_mask), _ptr(row_mask),
+            ENC_FWD_ONLINE_ATTENTION if online_attention else 0, _stream(x.device),
         ),
     )
