@@ -129,6 +129,14 @@ int enc_attention_online_fwd_bf16(const void* q, const void* k, const void* v_t,
                                   const int32_t* kv_len,
                                   const uint8_t* key_mask, void* stream);
 
+/* Self-check of the attention's softmax exponential (no counterpart in the
+ * reference; for test suites): adds to *mismatches (a device uint32 the
+ * caller zeroes) the number of float bit patterns in [lo_bits, hi_bits]
+ * (non-positive floats, e.g. 0x80000000 .. 0xc2d00000 = -0 .. -104) where the
+ * exact attention's inlined exp differs from the device library's expf. */
+int enc_selfcheck_expf(uint32_t lo_bits, uint32_t hi_bits, uint32_t* mismatches,
+                       void* stream);
+
 /* kv_len[b] = number of valid tokens in mask[b, :] (int32, device).  Equal to
  * the prefix length for the prefix masks built by generate_random_case
  * (transformer_benchmark/cases.py:87-97). */

@@ -207,6 +207,14 @@ def test_qkv_head_major(device, b, s, d, h):
     assert bitwise_fraction(packed[0], q) > 0.999 and bitwise_fraction(packed[1], k) > 0.999
 
 
+def test_softmax_exp_matches_device_expf_exhaustively(device):
+    """The exact attention's inlined exp equals the device library's expf on
+    every float in [-104, -0] (below -103.28 both return 0) and at -inf."""
+    assert native.selfcheck_expf(0x80000000, 0xC2D00000, device) == 0
+    assert native.selfcheck_expf(0xFF800000, 0xFF800000, device) == 0  # -inf
+    assert native.selfcheck_expf(0x00000000, 0x00000000, device) == 0  # +0
+
+
 def _attention_inputs(device, b, h, s, seed):
     g = torch.Generator(device=device).manual_seed(seed)
     q = torch.randn(b, h, s, 64, generator=g, device=device).bfloat16()

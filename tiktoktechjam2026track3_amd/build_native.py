@@ -41,6 +41,16 @@ COMMON_FLAGS = (
 )
 
 
+# Per-source extra flags.  The attention kernels read every score accumulator
+# with VALU instructions; keeping MFMA results in VGPRs (not AGPRs) saves a
+# v_accvgpr_read per score.  The GEMM keeps the compiler's choice: its large
+# accumulator tiles live in AGPRs.
+EXTRA_FLAGS = {
+    "attention.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form"),
+    "flash_attention.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form"),
+}
+
+
 def _hipcc() -> str:
     candidate = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not Path(candidate).exists():
@@ -71,7 +81,8 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
         src = CSRC_DIR / name
         obj = BUILD_DIR / (src.stem + ".o")
         objects.append(obj)
-        commands.append([hipcc, *COMMON_FLAGS, include, "-c", str(src), "-o", str(obj)])
+        extra = EXTRA_FLAGS.get(name, ())
+        commands.append([hipcc, *COMMON_FLAGS, *extra, include, "-c", str(src), "-o", str(obj)])
     workers = jobs or min(len(commands), max(1, (os.cpu_count() or 2)))
     if verbose:
         for cmd in commands:

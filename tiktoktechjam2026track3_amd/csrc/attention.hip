@@ -1,9 +1,10 @@
 // Streaming multi-head attention forward for gfx950, head_dim = 64, bitwise
 // equal to the reference's materialised softmax attention.
 //
-// Scores are never materialised: each workgroup owns BQ = 128 query rows of one
-// (batch, head) (32 per wavefront) and streams 64-key tiles of K (and V^T)
-// through double-buffered LDS.  Both products put the query on the MFMA N
+// Scores are never materialised: each workgroup owns BQ = NW * 32 query rows
+// of one (batch, head) (32 per wavefront) and streams 64-key tiles of K (and
+// V^T) through a two-stage LDS ring filled with direct global->LDS loads
+// (global_load_lds_dwordx4).  Both products put the query on the MFMA N
 // dimension (the lane), so every per-query quantity lives in the lane that owns
 // the query (lane l: query l%32, key half l/32):
 //   S^T[key, q]  = K[key, :] . Q[q, :]        A = K tile (LDS), B = Q (registers)
@@ -19,7 +20,7 @@
 //   p = bf16(softmax_fp32(s))                   (torch.softmax in fp32, then bf16)
 //   context = bf16(sum_j p_j v_j)               (MFMA, fp32 accumulate)
 // torch's ROCm softmax computes p differently for the two row-length regimes:
-//   rows of <= 2048 keys: e = expf(s - max) (libm-accurate), p = e / sum;
+//   rows of <= 2048 keys: e = expf(s - max) (device-library expf), p = e / sum;
 //   longer rows:          e = exp2(rn(s - max) * log2(e)) on the hardware exp
 //                         unit, p = e * (1 / sum) with a correctly rounded 1 / sum.
 // The softmax sum is accumulated in the order torch's ROCm softmax uses:
@@ -31,6 +32,17 @@
 // Both orders were pinned against torch.softmax on an MI355X by fingerprinting
 // the reduction tree.  Because p is rounded after normalisation, the kernel
 // sweeps the keys three times: (A) row max, (B) row sum, (C) probabilities + PV.
+//
+// Cost notes.  The kernel is bound by VALU work per score, not by the MFMAs:
+//   * sweep A takes the max of the raw fp32 dot products and rounds it once at
+//     the end; rounding to bf16 (and scaling by a positive scale) is monotonic,
+//     so max(bf16(x)) = bf16(max(x));
+//   * the division of the short-row regime, p = RN(e / sum), is evaluated as
+//     q0 = RN(e * r), rem = fma(-q0, sum, e), p = fma(rem, r, q0) with
+//     r = RN(1 / sum): Markstein's correction step, which gives the correctly
+//     rounded quotient whenever no intermediate underflows.  Rows whose
+//     smallest weight could underflow (min s - max < -69, e < 2^-100) use the
+//     IEEE division instead (one branch per wavefront).
 // In sweep B for long rows, tiles are visited residue-major (tile n = r + 32m,
 // r = 0..31) so each 512-thread "thread" partial is completed in key order and
 // each warp's 64 partials are live in registers only while that warp is summed.
@@ -39,7 +51,8 @@
 // last query can see, and a wavefront skips the MFMAs of tiles in its future;
 // with prefix padding (kv_len) key tiles past kv_len are never loaded and query
 // tiles past kv_len are written as zeros.  Skipped keys contribute exp(-inf) = 0
-// in the reference, so skipping them is exact.
+// in the reference, and adding 0 leaves a partial sum unchanged, so skipping
+// them is exact.
 #include "common.h"
 #include "kernels.h"
 
@@ -48,24 +61,23 @@ namespace enc {
 namespace {
 
 constexpr int kHd = 64;
-constexpr int kBQ = 128;      // queries per workgroup (32 per wavefront)
-constexpr int kBKV = 64;      // keys per tile
-constexpr int kLds = 64 + 8;  // padded LDS row (elements)
-constexpr int kThreads = 256;
+constexpr int kBKV = 64;                   // keys per tile
+constexpr int kTileElems = kBKV * kHd;     // one K or V^T tile, bf16 elements
 constexpr int kWarpSoftmaxMaxKeys = 2048;  // rows up to this length use the warp order
 constexpr float kLog2e = 1.44269504088896340736f;
-
-// exp of (s - max) as the softmax of the given regime computes it.
-template <bool BLOCK_ORDER>
-__device__ __forceinline__ float softmax_exp(float x) {
-  if constexpr (BLOCK_ORDER) {
-    return __builtin_amdgcn_exp2f(x * kLog2e);
-  } else {
-    return expf(x);
-  }
-}
+// below this weight (s - max < -69.3) the Markstein quotient is not used
+constexpr float kMinFastGap = -69.0f;
 
 enum MaskMode : int { kMaskNone = 0, kMaskPrefix = 1, kMaskBytes = 2 };
+
+// LDS tile = 64 rows (keys of K, head channels of V^T) x 8 chunks of 16 bytes.
+// Chunk c of row r sits in slot c ^ (r & 7), so the 32 rows one MFMA fragment
+// read touches at a fixed chunk fall in distinct bank groups.
+__device__ __forceinline__ int tile_off(int row, int chunk) { return row * kHd + ((chunk ^ (row & 7)) << 3); }
+
+// s_waitcnt immediate: wait until no vector-memory operation is outstanding
+// (expcnt and lgkmcnt left at their no-wait maxima; gfx9 encoding).
+constexpr int kWaitVm0 = (7 << 4) | (15 << 8);
 
 // key offset inside a 64-key tile held by accumulator register r of block kb32
 // in lane half h (see the permutation above)
@@ -74,27 +86,35 @@ __device__ __forceinline__ int tile_key(int kb32, int r, int h) {
   return 32 * kb32 + 16 * (i >> 1) + 8 * h + 4 * (i & 1) + j;
 }
 
-template <bool CAUSAL, int MASK, bool POW2_SCALE, bool BLOCK_ORDER>
-__global__ void __launch_bounds__(kThreads)
+template <int NW, bool CAUSAL, int MASK, bool POW2_SCALE, bool BLOCK_ORDER>
+__global__ void __launch_bounds__(NW * kWave)
 attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
                      const bf16_t* __restrict__ Vt, bf16_t* __restrict__ ctx, int H, int S,
                      int ld_vt, int num_qblocks, float scale,
                      const int32_t* __restrict__ kv_len, const uint8_t* __restrict__ key_mask) {
-  __shared__ __attribute__((aligned(16))) bf16_t sK[2][kBKV * kLds];
-  __shared__ __attribute__((aligned(16))) bf16_t sV[2][kHd * kLds];
+  constexpr int kThreads = NW * kWave;
+  constexpr int kBQ = NW * 32;
+  __shared__ __attribute__((aligned(16))) bf16_t sK[2][kTileElems];
+  __shared__ __attribute__((aligned(16))) bf16_t sV[2][kTileElems];
   __shared__ uint8_t sM[2][kBKV];
 
-  // 1D grid.  Non-causal: consecutive workgroups are consecutive query tiles of
-  // one head, so the resident workgroups stream the same K/V and share it in L2.
-  // Causal: heads vary fastest and query tiles run last-to-first, so the
-  // heaviest tiles (which see the most keys) start first.
-  const int id = blockIdx.x;
-  const int num_bh = static_cast<int>(gridDim.x) / num_qblocks;
+  // Block -> (batch*head, query tile).  Non-causal: MI355X hands consecutive
+  // workgroups to its 8 XCDs round-robin; the id is remapped so each XCD walks
+  // a contiguous run of query tiles of one head, whose K/V then stream through
+  // that XCD's L2 once for all of them.  Causal: heads vary fastest and query
+  // tiles run last-to-first, so the heaviest tiles (most keys) start first.
+  const int nblocks = static_cast<int>(gridDim.x);
+  const int num_bh = nblocks / num_qblocks;
   int bh, qb;
   if constexpr (CAUSAL) {
+    const int id = blockIdx.x;
     bh = id % num_bh;
     qb = num_qblocks - 1 - id / num_bh;
   } else {
+    const int pid = blockIdx.x;
+    const int xcd = pid % 8, slot = pid / 8;
+    const int base = nblocks / 8, rem = nblocks % 8;
+    const int id = xcd * base + min(xcd, rem) + slot;
     qb = id % num_qblocks;
     bh = id / num_qblocks;
   }
@@ -105,7 +125,8 @@ attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg
 
   const int tid = threadIdx.x;
   const int lane = tid % kWave;
-  const int wave = tid / kWave;
+  // wavefront index as a scalar, so per-tile decisions stay uniform branches
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int l32 = lane & 31;
   const int lhi = lane >> 5;
   const int qrow = q0 + wave * 32 + l32;  // the query this lane owns
@@ -150,68 +171,66 @@ attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg
   // MFMA row l32 of a 32-key block reads K row perm(l32)
   const int krow = 16 * ((l32 >> 3) >> 1) + 8 * ((l32 >> 2) & 1) + 4 * ((l32 >> 3) & 1) + (l32 & 3);
 
-  // Tile loader: K tile = 64 keys x 64 d (512 x 16B chunks), V^T tile = 64 d x
-  // 64 keys (512 chunks); 256 threads -> 2 chunks of each per thread.
-  u32x4 rk[2], rv[2];
-  uint32_t rm = 0;
-  auto load_tile = [&](int kb, bool with_v) {
-    const int k0 = kb * kBKV;
+  // ---- tile loads ----
+  // Full tiles: load instruction j of wavefront w fills LDS rows 8(NW j + w) ..
+  // +7 (64 lanes x 16 bytes, consecutive); lane L writes row 8(NW j + w) + L/8,
+  // slot L%8, which holds chunk (L%8) ^ (L/8) of that row.
+  const int ld_row = lane >> 3;
+  const int ld_chunk = (lane & 7) ^ ld_row;
+  auto issue_full = [&](int buf, int k0, bool with_v) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int c = tid + i * kThreads;
-      const int row = c >> 3;  // key (K) or d (V^T)
-      const int cc = c & 7;    // 16B chunk within the row
-      const int key = k0 + row;
-      if (key < S) {
-        rk[i] = *reinterpret_cast<const u32x4*>(Kh + static_cast<int64_t>(key) * kHd + cc * 8);
-      } else {
-        rk[i] = u32x4{0, 0, 0, 0};
-      }
-      if (!with_v) continue;
-      const int kv0 = k0 + cc * 8;
-      const bf16_t* vp = Vh + static_cast<int64_t>(row) * ld_vt + kv0;
-      if (kv0 + 8 <= S) {
-        rv[i] = *reinterpret_cast<const u32x4*>(vp);
-      } else {
-        uint16_t tmp[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) tmp[e] = (kv0 + e < S) ? vp[e] : uint16_t(0);
-        rv[i] = u32x4{tmp[0] | (uint32_t(tmp[1]) << 16), tmp[2] | (uint32_t(tmp[3]) << 16),
-                      tmp[4] | (uint32_t(tmp[5]) << 16), tmp[6] | (uint32_t(tmp[7]) << 16)};
-      }
-    }
-    if constexpr (MASK == kMaskBytes) {
-      if (tid < kBKV) {
-        const int key = k0 + tid;
-        rm = (key < S) ? Mh[key] : 0;
-      }
+    for (int j = 0; j < 8 / NW; ++j) {
+      const int row0 = 8 * (NW * j + wave);
+      const int row = row0 + ld_row;
+      __builtin_amdgcn_global_load_lds(Kh + static_cast<int64_t>(k0 + row) * kHd + ld_chunk * 8,
+                                       &sK[buf][row0 * kHd], 16, 0, 0);
+      if (with_v)
+        __builtin_amdgcn_global_load_lds(Vh + static_cast<int64_t>(row) * ld_vt + k0 + ld_chunk * 8,
+                                         &sV[buf][row0 * kHd], 16, 0, 0);
     }
   };
-  auto store_tile = [&](int buf, bool with_v) {
+  // The tile that crosses seq_len goes through registers: keys >= S read as
+  // zeros (V^T's padding columns are never read, so they may hold anything).
+  auto load_edge = [&](int buf, int k0, bool with_v) {
+    for (int c = tid; c < kBKV * 8; c += kThreads) {
+      const int row = c >> 3, chunk = c & 7;
+      u32x4 kv = u32x4{0, 0, 0, 0};
+      if (k0 + row < S) kv = *reinterpret_cast<const u32x4*>(Kh + static_cast<int64_t>(k0 + row) * kHd + chunk * 8);
+      *reinterpret_cast<u32x4*>(&sK[buf][tile_off(row, chunk)]) = kv;
+      if (!with_v) continue;
+      const int key = k0 + chunk * 8;
+      const bf16_t* vp = Vh + static_cast<int64_t>(row) * ld_vt + key;
+      uint16_t t[8];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int c = tid + i * kThreads;
-      *reinterpret_cast<u32x4*>(&sK[buf][(c >> 3) * kLds + (c & 7) * 8]) = rk[i];
-      if (with_v) *reinterpret_cast<u32x4*>(&sV[buf][(c >> 3) * kLds + (c & 7) * 8]) = rv[i];
+      for (int e = 0; e < 8; ++e) t[e] = (key + e < S) ? vp[e] : uint16_t(0);
+      *reinterpret_cast<u32x4*>(&sV[buf][tile_off(row, chunk)]) =
+          u32x4{t[0] | (uint32_t(t[1]) << 16), t[2] | (uint32_t(t[3]) << 16),
+                t[4] | (uint32_t(t[5]) << 16), t[6] | (uint32_t(t[7]) << 16)};
+    }
+  };
+  auto issue_tile = [&](int buf, int kb, bool with_v) {
+    const int k0 = kb * kBKV;
+    if (k0 + kBKV <= S) {
+      issue_full(buf, k0, with_v);
+    } else {
+      load_edge(buf, k0, with_v);
     }
     if constexpr (MASK == kMaskBytes) {
-      if (tid < kBKV) sM[buf][tid] = static_cast<uint8_t>(rm);
+      if (tid < kBKV) sM[buf][tid] = (k0 + tid < S) ? Mh[k0 + tid] : uint8_t(0);
     }
   };
 
   // Runs body(buf, tile) over nkb tiles in the order seq(0), seq(1), ...,
   // double-buffered: the loads of the next tile overlap the current body.
   auto sweep = [&](auto seq, bool with_v, auto body) {
-    if (nkb > 0) {
-      load_tile(seq(0), with_v);
-      store_tile(0, with_v);
-    }
+    if (nkb > 0) issue_tile(0, seq(0), with_v);
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
     __syncthreads();
     for (int it = 0; it < nkb; ++it) {
       const int cur = it & 1;
-      if (it + 1 < nkb) load_tile(seq(it + 1), with_v);
+      if (it + 1 < nkb) issue_tile(cur ^ 1, seq(it + 1), with_v);
       body(cur, seq(it));
-      if (it + 1 < nkb) store_tile(cur ^ 1, with_v);
+      __builtin_amdgcn_s_waitcnt(kWaitVm0);
       __syncthreads();
     }
   };
@@ -219,58 +238,119 @@ attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg
   const int wq_first = q0 + wave * 32;
   const int wq_last = wq_first + 31;
 
-  // Score tile (64 keys x 32 queries) of LDS buffer `buf` into s[2]: the
-  // reference's fp32 view of its bf16 scores, excluded keys = -inf.
-  auto tile_scores = [&](int buf, int k0, f32x16 (&s)[2]) {
+  // Raw fp32 dot products of the 64-key tile in LDS buffer `buf`.
+  auto tile_dots = [&](int buf, f32x16 (&s)[2]) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       s[0][r] = 0.f;
       s[1][r] = 0.f;
     }
 #pragma unroll
-    for (int kb32 = 0; kb32 < 2; ++kb32) {
+    for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(
-            &sK[buf][(kb32 * 32 + krow) * kLds + ks * 16 + lhi * 8]);
+      for (int kb32 = 0; kb32 < 2; ++kb32) {
+        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&sK[buf][tile_off(kb32 * 32 + krow, 2 * ks + lhi)]);
         s[kb32] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], s[kb32], 0, 0, 0);
       }
     }
-    const bool need_mask = (CAUSAL && k0 + kBKV - 1 > wq_first) || (k0 + kBKV > kv_limit) ||
-                           (MASK == kMaskBytes);
+  };
+  // Whether key (tile offset kl) is allowed for this lane's query.
+  auto key_ok = [&](int buf, int k0, int kl) {
+    const int key = k0 + kl;
+    bool ok = key < kv_limit;
+    if constexpr (CAUSAL) ok = ok && key <= qrow;
+    if constexpr (MASK == kMaskBytes) ok = ok && sM[buf][kl] != 0;
+    return ok;
+  };
+  auto tile_needs_mask = [&](int k0) {
+    return (CAUSAL && k0 + kBKV - 1 > wq_first) || (k0 + kBKV > kv_limit) || (MASK == kMaskBytes);
+  };
+  // Score tile into s[2] as the softmax's first operation sees it:
+  //   g = rn(s - max), s = bf16(bf16(q.k) * scale), excluded keys -inf.
+  // With a power-of-two scale, s = bf16(q.k) * scale exactly and
+  // rn(s - max) = scale * rn(bf16(q.k) - bf16(max raw dot)), so the scale
+  // multiplies the difference (or folds into the exp2 multiplier below).
+  // gap_scaled selects whether the returned g carries the scale.
+  auto tile_gaps = [&](int buf, int k0, float row_max, float raw_max_bf, bool gap_scaled,
+                       f32x16 (&s)[2]) {
+    tile_dots(buf, s);
 #pragma unroll
     for (int kb32 = 0; kb32 < 2; ++kb32) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float rq = round_bf16(s[kb32][r]);
-        float v = POW2_SCALE ? rq * scale : round_bf16(rq * scale);
-        if (need_mask) {
-          const int kl = tile_key(kb32, r, lhi);
-          const int key = k0 + kl;
-          bool ok = key < kv_limit;
-          if constexpr (CAUSAL) ok = ok && key <= qrow;
-          if constexpr (MASK == kMaskBytes) ok = ok && sM[buf][kl] != 0;
-          v = ok ? v : -INFINITY;
+      for (int r = 0; r < 16; r += 2) {
+        const uint32_t pk = pack_bf16x2(s[kb32][r], s[kb32][r + 1]);
+        float v0 = lo_bf16(pk), v1 = hi_bf16(pk);
+        if constexpr (POW2_SCALE) {
+          v0 = v0 - raw_max_bf;
+          v1 = v1 - raw_max_bf;
+          if (gap_scaled) {
+            v0 *= scale;
+            v1 *= scale;
+          }
+        } else {
+          v0 = round_bf16(v0 * scale) - row_max;
+          v1 = round_bf16(v1 * scale) - row_max;
         }
-        s[kb32][r] = v;
+        s[kb32][r] = v0;
+        s[kb32][r + 1] = v1;
       }
+    }
+    if (tile_needs_mask(k0)) {
+#pragma unroll
+      for (int kb32 = 0; kb32 < 2; ++kb32)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          s[kb32][r] = key_ok(buf, k0, tile_key(kb32, r, lhi)) ? s[kb32][r] : -INFINITY;
     }
   };
   auto natural = [](int it) { return it; };
 
   // ============================ sweep A: row max ============================
-  float m_lane = -INFINITY;
+  // max (and, for the short-row regime, min) of the raw dot products of the
+  // allowed keys; the bf16 score of the max is formed once afterwards.
+  float mx = -INFINITY, mn = INFINITY;
   sweep(natural, false, [&](int buf, int kb) {
     const int k0 = kb * kBKV;
     if (CAUSAL && k0 > wq_last) return;
     f32x16 s[2];
-    tile_scores(buf, k0, s);
+    tile_dots(buf, s);
+    if (tile_needs_mask(k0)) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) m_lane = fmaxf(m_lane, fmaxf(s[0][r], s[1][r]));
+      for (int kb32 = 0; kb32 < 2; ++kb32) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const bool ok = key_ok(buf, k0, tile_key(kb32, r, lhi));
+          mx = fmaxf(mx, ok ? s[kb32][r] : -INFINITY);
+          if constexpr (!BLOCK_ORDER) mn = fminf(mn, ok ? s[kb32][r] : INFINITY);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) {
+        mx = fmaxf(mx, fmaxf(fmaxf(s[0][r], s[0][r + 1]), fmaxf(s[1][r], s[1][r + 1])));
+        if constexpr (!BLOCK_ORDER) mn = fminf(mn, fminf(fminf(s[0][r], s[0][r + 1]), fminf(s[1][r], s[1][r + 1])));
+      }
+    }
   });
-  const float row_max = fmaxf(m_lane, __shfl_xor(m_lane, 32, kWave));
+  mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+  auto to_score = [&](float raw) {
+    const float rq = round_bf16(raw);
+    return POW2_SCALE ? rq * scale : round_bf16(rq * scale);
+  };
+  const float row_max = (mx == -INFINITY) ? -INFINITY : to_score(mx);
+  const float raw_max_bf = (mx == -INFINITY) ? -INFINITY : round_bf16(mx);
+  // exp2 multiplier of the long-row regime: log2(e), times the scale when the
+  // gap is kept unscaled (exact: the scale is a power of two)
+  const float c_exp = POW2_SCALE ? scale * kLog2e : kLog2e;
+  bool slow_div = false;
+  if constexpr (!BLOCK_ORDER) {
+    mn = fminf(mn, __shfl_xor(mn, 32, kWave));
+    // weights below 2^-100 could underflow inside the Markstein quotient
+    const bool tiny = (mn != INFINITY) && (to_score(mn) - row_max < kMinFastGap);
+    slow_div = __builtin_amdgcn_ballot_w64(tiny) != 0;
+  }
 
-  // ======================= sweep B: row sum of expf(s - max) =======================
+  // ======================= sweep B: row sum of exp(s - max) =======================
   float row_sum;
   if constexpr (!BLOCK_ORDER) {
     // warp order: partial[lam] over keys lam, lam+64, ... (lam = key % 64)
@@ -284,11 +364,11 @@ attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg
       const int k0 = kb * kBKV;
       if (CAUSAL && k0 > wq_last) return;
       f32x16 s[2];
-      tile_scores(buf, k0, s);
+      tile_gaps(buf, k0, row_max, raw_max_bf, true, s);
 #pragma unroll
       for (int kb32 = 0; kb32 < 2; ++kb32)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) part[kb32][r] += softmax_exp<false>(s[kb32][r] - row_max);
+        for (int r = 0; r < 16; ++r) part[kb32][r] += expf_nonpos(s[kb32][r]);
     });
     // 64-lane butterfly; lam bits: 5 = kb32, 4 = i>>1 (reg bit 3), 3 = lane half,
     // 2 = i&1 (reg bit 2), 1..0 = j (reg bits 1..0)
@@ -308,7 +388,10 @@ attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg
   } else {
     // block order: "thread" t (of 512) sums 4-key vectors t, t+512, ...; tile
     // n = r + 32 m holds the vectors of threads 16 r .. 16 r + 15.  Tiles are
-    // visited residue-major; "warp" w covers residues 4w .. 4w+3.
+    // visited residue-major; "warp" w covers residues 4w .. 4w+3.  All partial
+    // arrays are indexed statically: the running residue's partials live in
+    // acc[], a finished residue is shifted into hist[] (oldest first), and a
+    // finished warp's sum is shifted into warp_sum[].
     auto resmajor = [&](int it) {
       int r = 0;
       int acc = 0;
@@ -320,69 +403,68 @@ attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg
       }
     };
     float warp_sum[8];
-    float part[4][8];  // [residue within warp][vector slot 4*kb32 + i]
+    float hist[4][8];  // the current warp's finished residues, in order
+    float acc[8];      // [vector slot 4*kb32 + i] of the running residue
 #pragma unroll
     for (int w = 0; w < 8; ++w) warp_sum[w] = 0.f;
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
+    for (int v = 0; v < 8; ++v) {
+      acc[v] = 0.f;
 #pragma unroll
-      for (int v = 0; v < 8; ++v) part[q][v] = 0.f;
-    int cur_warp = 0;
-    auto flush_warp = [&](int w) {
-      // shuffle-down tree over lam = 16 rr + u, u = 8 kb32 + 4 (i>>1) + 2 h + (i&1):
-      // offsets 32, 16 (rr), 8 (kb32), 4 (i>>1), 2 (lane half), 1 (i&1)
-      float t8[8];
+      for (int q = 0; q < 4; ++q) hist[q][v] = 0.f;
+    }
+    int cur_res = 0;
+    // residue cur_res is complete: shift it into hist; after a warp's fourth
+    // residue, reduce the warp with a shuffle-down tree over
+    // lam = 16 rr + u, u = 8 kb32 + 4 (i>>1) + 2 h + (i&1):
+    // offsets 32, 16 (rr), 8 (kb32), 4 (i>>1), 2 (lane half), 1 (i&1)
+    auto finish_residue = [&]() {
 #pragma unroll
-      for (int v = 0; v < 8; ++v) t8[v] = (part[0][v] + part[2][v]) + (part[1][v] + part[3][v]);
-      float t4[4];
+      for (int v = 0; v < 8; ++v) {
+        hist[0][v] = hist[1][v];
+        hist[1][v] = hist[2][v];
+        hist[2][v] = hist[3][v];
+        hist[3][v] = acc[v];
+        acc[v] = 0.f;
+      }
+      ++cur_res;
+      if ((cur_res & 3) == 0) {
+        float t8[8];
 #pragma unroll
-      for (int v = 0; v < 4; ++v) t4[v] = t8[v] + t8[v + 4];                   // offset 8 (kb32)
-      float t2[2];
+        for (int v = 0; v < 8; ++v) t8[v] = (hist[0][v] + hist[2][v]) + (hist[1][v] + hist[3][v]);
+        float t4[4];
 #pragma unroll
-      for (int v = 0; v < 2; ++v) t2[v] = t4[v] + t4[v + 2];                   // offset 4 (i>>1)
+        for (int v = 0; v < 4; ++v) t4[v] = t8[v] + t8[v + 4];                   // offset 8 (kb32)
+        float t2[2];
 #pragma unroll
-      for (int v = 0; v < 2; ++v) t2[v] = t2[v] + __shfl_xor(t2[v], 32, kWave);  // offset 2
-      const float ws = t2[0] + t2[1];                                          // offset 1 (i&1)
+        for (int v = 0; v < 2; ++v) t2[v] = t4[v] + t4[v + 2];                   // offset 4 (i>>1)
 #pragma unroll
-      for (int ww = 0; ww < 8; ++ww)
-        if (ww == w) warp_sum[ww] = ws;
+        for (int v = 0; v < 2; ++v) t2[v] = t2[v] + __shfl_xor(t2[v], 32, kWave);  // offset 2
+        const float ws = t2[0] + t2[1];                                          // offset 1 (i&1)
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-#pragma unroll
-        for (int v = 0; v < 8; ++v) part[q][v] = 0.f;
+        for (int w = 0; w < 7; ++w) warp_sum[w] = warp_sum[w + 1];
+        warp_sum[7] = ws;
+      }
     };
     sweep(resmajor, false, [&](int buf, int kb) {
       const int k0 = kb * kBKV;
       const int r = kb & 31;
-      const int w = r >> 2;
-      while (cur_warp < w) {  // warps whose residues are complete are reduced
-        flush_warp(cur_warp);
-        ++cur_warp;
-      }
+      while (cur_res < r) finish_residue();  // uniform
       if (CAUSAL && k0 > wq_last) return;
       f32x16 s[2];
-      tile_scores(buf, k0, s);
-      const int rr = r & 3;
+      tile_gaps(buf, k0, row_max, raw_max_bf, false, s);
 #pragma unroll
       for (int kb32 = 0; kb32 < 2; ++kb32) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          float acc = 0.f;
+          float a = acc[4 * kb32 + i];
 #pragma unroll
-          for (int q = 0; q < 4; ++q)
-            if (q == rr) acc = part[q][4 * kb32 + i];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) acc += softmax_exp<true>(s[kb32][4 * i + j] - row_max);
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-            if (q == rr) part[q][4 * kb32 + i] = acc;
+          for (int j = 0; j < 4; ++j) a += __builtin_amdgcn_exp2f(s[kb32][4 * i + j] * c_exp);
+          acc[4 * kb32 + i] = a;
         }
       }
     });
-    while (cur_warp < 8) {
-      flush_warp(cur_warp);
-      ++cur_warp;
-    }
+    while (cur_res < 32) finish_residue();
     // tree over the 8 warp sums (offsets 4, 2, 1)
     const float a0 = warp_sum[0] + warp_sum[4], a1 = warp_sum[1] + warp_sum[5];
     const float a2 = warp_sum[2] + warp_sum[6], a3 = warp_sum[3] + warp_sum[7];
@@ -390,7 +472,9 @@ attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg
   }
 
   // ================== sweep C: p = bf16(softmax), context += P V ==================
-  const float inv_sum = 1.0f / row_sum;  // block-order epilogue multiplies by it
+  // Correctly rounded 1 / sum: the block-order epilogue multiplies by it; the
+  // short-row regime uses it as the Markstein reciprocal.
+  const float inv_sum = 1.0f / row_sum;
   f32x16 o[2];
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
@@ -401,23 +485,39 @@ attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg
     const int k0 = kb * kBKV;
     if (CAUSAL && k0 > wq_last) return;
     f32x16 s[2];
-    tile_scores(buf, k0, s);
+    tile_gaps(buf, k0, row_max, raw_max_bf, !BLOCK_ORDER, s);
     bf16x8 pf[4];
+    if (BLOCK_ORDER || !slow_div) {
 #pragma unroll
-    for (int kb32 = 0; kb32 < 2; ++kb32) {
+      for (int kb32 = 0; kb32 < 2; ++kb32) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float e = softmax_exp<BLOCK_ORDER>(s[kb32][r] - row_max);
-        const float p = BLOCK_ORDER ? e * inv_sum : e / row_sum;
-        pf[kb32 * 2 + (r >> 3)][r & 7] = static_cast<__bf16>(p);
+        for (int r = 0; r < 16; ++r) {
+          const float e = BLOCK_ORDER ? __builtin_amdgcn_exp2f(s[kb32][r] * c_exp) : expf_nonpos(s[kb32][r]);
+          float p;
+          if constexpr (BLOCK_ORDER) {
+            p = e * inv_sum;
+          } else {
+            const float q = e * inv_sum;
+            p = fmaf(fmaf(-q, row_sum, e), inv_sum, q);
+          }
+          pf[kb32 * 2 + (r >> 3)][r & 7] = static_cast<__bf16>(p);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int kb32 = 0; kb32 < 2; ++kb32) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float e = expf_nonpos(s[kb32][r]);
+          pf[kb32 * 2 + (r >> 3)][r & 7] = static_cast<__bf16>(e / row_sum);
+        }
       }
     }
 #pragma unroll
-    for (int db = 0; db < 2; ++db) {
+    for (int kk = 0; kk < 4; ++kk) {
 #pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        const bf16x8 vf = *reinterpret_cast<const bf16x8*>(
-            &sV[buf][(db * 32 + l32) * kLds + 16 * kk + 8 * lhi]);
+      for (int db = 0; db < 2; ++db) {
+        const bf16x8 vf = *reinterpret_cast<const bf16x8*>(&sV[buf][tile_off(db * 32 + l32, 2 * kk + lhi)]);
         o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[kk], o[db], 0, 0, 0);
       }
     }
@@ -443,14 +543,15 @@ attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg
   }
 }
 
-template <bool CAUSAL, int MASK, bool POW2, bool BLOCK_ORDER>
+template <int NW, bool CAUSAL, int MASK, bool POW2, bool BLOCK_ORDER>
 hipError_t launch_attn(const bf16_t* q, const bf16_t* k, const bf16_t* vt, bf16_t* ctx, int B,
                        int H, int S, float scale, const int32_t* kv_len, const uint8_t* key_mask,
                        hipStream_t st) {
+  constexpr int kBQ = NW * 32;
   const int nqb = (S + kBQ - 1) / kBQ;
   const dim3 grid(static_cast<uint32_t>(B) * H * nqb);
   const int ld_vt = static_cast<int>(vt_stride(S));
-  hipLaunchKernelGGL((attn_fwd_hd64_kernel<CAUSAL, MASK, POW2, BLOCK_ORDER>), grid, dim3(kThreads),
+  hipLaunchKernelGGL((attn_fwd_hd64_kernel<NW, CAUSAL, MASK, POW2, BLOCK_ORDER>), grid, dim3(NW * kWave),
                      0, st, q, k, vt, ctx, H, S, ld_vt, nqb, scale, kv_len, key_mask);
   return hipGetLastError();
 }
@@ -460,8 +561,13 @@ hipError_t dispatch_order(const bf16_t* q, const bf16_t* k, const bf16_t* vt, bf
                           int H, int S, float scale, const int32_t* kv_len,
                           const uint8_t* key_mask, hipStream_t st) {
   if (S > kWarpSoftmaxMaxKeys)
-    return launch_attn<CAUSAL, MASK, POW2, true>(q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
-  return launch_attn<CAUSAL, MASK, POW2, false>(q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
+    return launch_attn<4, CAUSAL, MASK, POW2, true>(q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
+  // Small problems use one-wavefront workgroups (32 queries) so more of the
+  // 256 CUs get work; larger ones share each K/V tile among 4 wavefronts.
+  const int64_t groups128 = static_cast<int64_t>(B) * H * ((S + 127) / 128);
+  if (groups128 < 512)
+    return launch_attn<1, CAUSAL, MASK, POW2, false>(q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
+  return launch_attn<4, CAUSAL, MASK, POW2, false>(q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
 }
 
 template <bool CAUSAL, int MASK>
@@ -495,7 +601,32 @@ mask_lengths_kernel(const uint8_t* __restrict__ mask, int64_t S, int32_t* __rest
   if (threadIdx.x == 0) kv_len[b] = partial[0] + partial[1] + partial[2] + partial[3];
 }
 
+// Compares expf_nonpos with the device library's expf on every float bit
+// pattern in [lo, hi] (unsigned order; pass patterns of non-positive floats).
+__global__ void __launch_bounds__(256)
+expf_check_kernel(uint32_t lo, uint32_t hi, uint32_t* __restrict__ mismatches) {
+  const uint64_t per_block = 256ull * 64ull;
+  const uint64_t first = lo + static_cast<uint64_t>(blockIdx.x) * per_block + threadIdx.x;
+  uint32_t bad = 0;
+  for (int i = 0; i < 64; ++i) {
+    const uint64_t bits = first + static_cast<uint64_t>(i) * 256ull;
+    if (bits > hi) break;
+    const float x = __uint_as_float(static_cast<uint32_t>(bits));
+    bad += __float_as_uint(expf_nonpos(x)) != __float_as_uint(expf(x));
+  }
+  if (bad) atomicAdd(mismatches, bad);
+}
+
 }  // namespace
+
+hipError_t expf_selfcheck(uint32_t lo_bits, uint32_t hi_bits, uint32_t* mismatches, hipStream_t stream) {
+  if (hi_bits < lo_bits) return hipErrorInvalidValue;
+  const uint64_t count = static_cast<uint64_t>(hi_bits) - lo_bits + 1;
+  const uint64_t blocks = (count + 256ull * 64ull - 1) / (256ull * 64ull);
+  hipLaunchKernelGGL(expf_check_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, stream, lo_bits,
+                     hi_bits, mismatches);
+  return hipGetLastError();
+}
 
 bool attention_seq_supported(int64_t seq_len) {
   // torch's long-row softmax folds 4-element vectors; other lengths are not pinned

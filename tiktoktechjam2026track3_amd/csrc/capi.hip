@@ -218,6 +218,14 @@ int enc_attention_online_fwd_bf16(const void* q, const void* k, const void* v_t,
                          key_mask, stream);
 }
 
+int enc_selfcheck_expf(uint32_t lo_bits, uint32_t hi_bits, uint32_t* mismatches, void* stream) {
+  if (!mismatches) return fail(ENC_ERR_INVALID, "selfcheck_expf: null counter");
+  if (hi_bits < lo_bits) return fail(ENC_ERR_INVALID, "selfcheck_expf: empty range");
+  hipError_t e = enc::expf_selfcheck(lo_bits, hi_bits, mismatches, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail_hip(e, "selfcheck_expf launch");
+  return ok();
+}
+
 int enc_mask_lengths(const uint8_t* mask, int64_t batch, int64_t seq_len, int32_t* kv_len, void* stream) {
   if (batch < 0 || seq_len < 0) return fail(ENC_ERR_INVALID, "mask_lengths: bad shape");
   if (batch == 0) return ok();

@@ -27,10 +27,13 @@ __device__ __forceinline__ bf16_t f32_to_bf16(float v) {
   return __builtin_bit_cast(bf16_t, h);
 }
 
-// Two floats -> packed bf16 pair (lo in bits 0..15).
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// Two floats -> packed bf16 pair (lo in bits 0..15), round to nearest even.
+// The vector conversion maps onto one v_cvt_pk_bf16_f32 for both values.
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  bf16x2 v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
-  return __builtin_bit_cast(uint32_t, v);
+  const f32x2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
 }
 
 // Round a float to the nearest bf16 value and return it as float.
@@ -40,6 +43,25 @@ __device__ __forceinline__ float round_bf16(float v) {
 
 __device__ __forceinline__ float lo_bf16(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float hi_bf16(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// expf(x) for x <= 0 (or -inf), bit for bit what the device library's expf
+// returns: the same operation sequence (x * log2(e) split into a rounded
+// product and an fma-recovered low part, nearest-integer split, v_exp_f32 of
+// the fraction, ldexp by the integer part) and the same underflow clamp to 0
+// below -103.28, without the overflow clamp, which cannot fire for x <= 0.
+// Softmax exponentials exp(s - max) are its only use.
+__device__ __forceinline__ float expf_nonpos(float x) {
+#pragma clang fp contract(off)
+  const float l2e = __uint_as_float(0x3fb8aa3bu);     // log2(e) rounded
+  const float l2e_lo = __uint_as_float(0x32a5705fu);  // log2(e) - l2e
+  const float ph = x * l2e;
+  float pl = __builtin_fmaf(x, l2e, -ph);
+  pl = __builtin_fmaf(x, l2e_lo, pl);
+  const float n = __builtin_rintf(ph);
+  const float f = (ph - n) + pl;
+  const float r = __builtin_amdgcn_ldexpf(__builtin_amdgcn_exp2f(f), static_cast<int>(n));
+  return (x < __uint_as_float(0xc2ce8ed0u)) ? 0.f : r;  // -103.27893
+}
 
 // Exact-erf GELU in fp32: 0.5 * x * (1 + erf(x / sqrt(2))).
 __device__ __forceinline__ float gelu_erf(float x) {

@@ -106,7 +106,8 @@ flash_attn_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ 
 
   const int tid = threadIdx.x;
   const int lane = tid % kWave;
-  const int wave = tid / kWave;
+  // wavefront index as a scalar, so per-tile decisions stay uniform branches
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int l32 = lane & 31;
   const int lhi = lane >> 5;
   const int qrow = q0 + wave * 32 + l32;  // the query this lane owns

@@ -69,6 +69,10 @@ hipError_t flash_attention_fwd_bf16(const bf16_t* q, const bf16_t* k, const bf16
 // Sequence lengths whose softmax summation order is reproduced exactly.
 bool attention_seq_supported(int64_t seq_len);
 
+// Counts (atomically, into *mismatches) the float bit patterns in
+// [lo_bits, hi_bits] where the attention's expf_nonpos differs from expf.
+hipError_t expf_selfcheck(uint32_t lo_bits, uint32_t hi_bits, uint32_t* mismatches, hipStream_t stream);
+
 hipError_t mask_lengths(const uint8_t* mask, int64_t batch, int64_t seq_len, int32_t* kv_len,
                         hipStream_t stream);
 

@@ -55,6 +55,7 @@ SIGNATURES = (
         ctypes.c_int,
         (_VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _F32, _I32, _VP, _VP, _VP),
     ),
+    ("enc_selfcheck_expf", ctypes.c_int, (ctypes.c_uint32, ctypes.c_uint32, _VP, _VP)),
     ("enc_mask_lengths", ctypes.c_int, (_VP, _I64, _I64, _VP, _VP)),
     ("enc_encoder_workspace_bytes", ctypes.c_int64, (_I64, _I64, _I64, _I64, _I64)),
     (
@@ -266,6 +267,17 @@ def attention(
         ),
     )
     return out
+
+
+def selfcheck_expf(lo_bits: int, hi_bits: int, device: torch.device) -> int:
+    """Number of float bit patterns in [lo_bits, hi_bits] where the exact
+    attention's inlined exponential differs from the device library's expf."""
+    counter = torch.zeros(1, dtype=torch.int32, device=device)
+    _check(
+        "enc_selfcheck_expf",
+        load_library().enc_selfcheck_expf(lo_bits, hi_bits, counter.data_ptr(), _stream(device)),
+    )
+    return int(counter.item())
 
 
 def mask_lengths(mask: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
