@@ -15,9 +15,11 @@ Reported beside the throughput:
     Each kernel's launches, with the inputs a forward driven launch by launch
     through the C ABI gives them (the sequence enc_encoder_forward_bf16
     issues), are timed back to back between hipEvents on the stream they run
-    on (torch's current stream); achieved = algorithmic FLOPs (or bytes) per
-    launch / mean launch duration, against the MI355X dense bf16 MFMA peak
-    (2.5 PFLOP/s) or HBM peak (8 TB/s);
+    on (torch's current stream).  A kernel whose algorithmic FLOPs per byte
+    fall below the ridge point (2.5 PFLOP/s / 8 TB/s = 312) is HBM-bound:
+    achieved = algorithmic bytes per launch / mean launch duration against
+    8 TB/s; otherwise achieved = algorithmic FLOPs per launch / mean duration
+    against the MI355X dense bf16 MFMA peak (2.5 PFLOP/s);
   * ``cpu_baseline``: the oracle's restatement of the reference forward
     (oracle/encoder_oracle.py) timed on the host CPU for a bounded sample.
 """
@@ -48,6 +50,8 @@ def parse_args(argv=None):
                    help="rounds over the layers' launches when timing each kernel")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--copy-calibration-mib", type=int, default=0,
+                   help="finish with a device copy of this many MiB (rocprof counter calibration)")
     return p.parse_args(argv)
 
 
@@ -56,7 +60,7 @@ def parse_args(argv=None):
 def profiled_forward(cfg, model, x, mask, native, torch, record):
     """The native forward's launch sequence (enc_encoder_forward_bf16 issues the
     same kernels in the same order) driven launch by launch through the C ABI,
-    with ``record(name, work, bound, fn)`` wrapping every launch."""
+    with ``record(name, (flops, bytes), fn)`` wrapping every launch."""
     b, s, d = cfg.batch_size, cfg.seq_len, cfg.d_model
     h, f, hd = cfg.num_heads, cfg.ffn_dim, cfg.d_model // cfg.num_heads
     t = b * s
@@ -68,32 +72,40 @@ def profiled_forward(cfg, model, x, mask, native, torch, record):
         attn_flops = 4.0 * b * d * s * (s + 1) / 2  # causal-live, padding not subtracted
     else:
         attn_flops = 4.0 * b * d * s * s
-    ln_bytes = 4.0 * t * d + 4.0 * d
+    e = 2.0  # bf16 bytes
+    # (algorithmic FLOPs, algorithmic HBM bytes) per launch: every operand read
+    # once and every result written once
+    ln_work = (0.0, 2 * e * t * d + 2 * e * d)
+    qkv_work = (2.0 * t * 3 * d * d, e * (t * d + 3 * d * d + 3 * d + 3 * t * d))
+    attn_work = (attn_flops, e * 4 * t * d)
+    out_work = (2.0 * t * d * d, e * (t * d + d * d + d + 2 * t * d))
+    ffn_in_work = (2.0 * t * f * d, e * (t * d + f * d + f + t * f))
+    ffn_out_work = (2.0 * t * d * f, e * (t * f + d * f + d + 2 * t * d))
     xa = x.reshape(t, d)
     for layer in model.layers:
         attn = layer.attention
-        xn = record("layernorm", ln_bytes, "hbm",
+        xn = record("layernorm", ln_work,
                     lambda: native.layernorm(xa, layer.norm1.weight, layer.norm1.bias, layer.norm1.eps))
-        q, k, v_t = record("qkv_proj", 2.0 * t * 3 * d * d, "mfma",
+        q, k, v_t = record("qkv_proj", qkv_work,
                            lambda: native.qkv_proj(xn.view(b, s, d), attn.qkv_proj.weight,
                                                    attn.qkv_proj.bias, h))
-        ctx = record("attention", attn_flops, "mfma",
+        ctx = record("attention", attn_work,
                      lambda: native.attention(q, k, v_t, hd**-0.5, cfg.causal, kv_len=kv_len))
-        xb = record("out_proj_residual", 2.0 * t * d * d, "mfma",
+        xb = record("out_proj_residual", out_work,
                     lambda: native.linear(ctx.view(t, d), attn.out_proj.weight, attn.out_proj.bias,
                                           native.ENC_EPI_BIAS_RESIDUAL_KEEP, residual=xa,
                                           row_mask=row_mask))
-        xn2 = record("layernorm", ln_bytes, "hbm",
+        xn2 = record("layernorm", ln_work,
                      lambda: native.layernorm(xb, layer.norm2.weight, layer.norm2.bias, layer.norm2.eps))
-        hid = record("ffn_in_gelu", 2.0 * t * f * d, "mfma",
+        hid = record("ffn_in_gelu", ffn_in_work,
                      lambda: native.linear(xn2, layer.ffn_in.weight, layer.ffn_in.bias,
                                            native.ENC_EPI_BIAS_GELU))
-        xa = record("ffn_out_residual", 2.0 * t * d * f, "mfma",
+        xa = record("ffn_out_residual", ffn_out_work,
                     lambda: native.linear(hid, layer.ffn_out.weight, layer.ffn_out.bias,
                                           native.ENC_EPI_BIAS_RESIDUAL_ZERO, residual=xb,
                                           row_mask=row_mask))
     fn = model.final_norm
-    return record("layernorm", ln_bytes, "hbm",
+    return record("layernorm", ln_work,
                   lambda: native.layernorm(xa, fn.weight, fn.bias, fn.eps, row_mask=row_mask)).view(b, s, d)
 
 
@@ -108,8 +120,11 @@ def kernel_profile(cfg, model, x, mask, native, torch, reps):
     (inter-launch gaps included, so it slightly overstates the kernel)."""
     launches = {}
 
-    def record(name, work, bound, fn):
-        entry = launches.setdefault(name, {"work": work, "bound": bound, "fns": []})
+    def record(name, work, fn):
+        flops, nbytes = work
+        # below the ridge point (peak FLOP/s over peak bytes/s) HBM bounds it
+        bound = "mfma" if flops / nbytes >= MFMA_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9) else "hbm"
+        entry = launches.setdefault(name, {"flops": flops, "bytes": nbytes, "bound": bound, "fns": []})
         entry["fns"].append(fn)
         return fn()
 
@@ -132,7 +147,8 @@ def kernel_profile(cfg, model, x, mask, native, torch, reps):
                 fn()
         end.record()
         torch.cuda.synchronize()
-        stats[name] = {"work": entry["work"], "bound": entry["bound"], "per_step": per_step[name],
+        stats[name] = {"flops": entry["flops"], "bytes": entry["bytes"], "bound": entry["bound"],
+                       "per_step": per_step[name],
                        "mean_ms": start.elapsed_time(end) / (reps * len(fns)),
                        "launches": reps * len(fns)}
     return stats, out
@@ -140,7 +156,8 @@ def kernel_profile(cfg, model, x, mask, native, torch, reps):
 
 def load_traffic(kernel, workload):
     """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE and
-    WRITE_SIZE runs, scaled by the copy-kernel calibration) if recorded."""
+    WRITE_SIZE runs, scaled by the copy-kernel calibration), if recorded in
+    profiles/traffic.json by ``python -m tiktoktechjam2026track3_amd.profiling``."""
     path = ROOT / "profiles" / "traffic.json"
     try:
         table = json.loads(path.read_text())
@@ -148,6 +165,20 @@ def load_traffic(kernel, workload):
         return None
     entry = table.get(f"{kernel}@{workload}")
     return None if entry is None else entry.get("bytes_per_launch")
+
+
+def copy_calibration(mib, torch):
+    """A device-to-device copy of exactly ``mib`` MiB, so a rocprofv3 --pmc run
+    of this process reads FETCH_SIZE / WRITE_SIZE for a kernel of known traffic
+    (the largest __amd_rocclr_copyBuffer dispatch)."""
+    n = mib * 1024 * 1024
+    src = torch.empty(n, dtype=torch.uint8, device="cuda")
+    src.fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
 
 
 # ----------------------------------------------------------- CPU baseline ----
@@ -250,10 +281,12 @@ def main(argv=None) -> int:
         stats, prof_out = kernel_profile(cfg, candidate, x, mask, native, torch, args.kernel_reps)
         if not torch.equal(prof_out, graph_out):
             print("warning: launch-by-launch forward differs from the model forward", file=sys.stderr)
+    if args.copy_calibration_mib > 0:
+        copy_calibration(args.copy_calibration_mib, torch)
     timed = []
     for name, v in stats.items():
         timed.append((v["per_step"] * v["mean_ms"], name, v["per_step"], v["mean_ms"], v["launches"],
-                      v["work"], v["bound"]))
+                      v["flops"], v["bytes"], v["bound"]))
     timed.sort(reverse=True)
 
     ms_per_step = total_ms / args.steps
@@ -262,25 +295,31 @@ def main(argv=None) -> int:
     attn = 4.0 * b * d * s * (s + 1) / 2 if cfg.causal else 4.0 * b * d * s * s
     flops = cfg.num_layers * (8.0 * tokens * d * d + 4.0 * tokens * d * f + attn)
 
-    _, kname, kcount, kmean, ktimed, kwork, kbound = timed[0]
-    achieved = kwork / (kmean * 1e-3) / (1e12 if kbound == "mfma" else 1e9)
-    peak = MFMA_PEAK_TFLOPS if kbound == "mfma" else HBM_PEAK_GBS
+    _, kname, kcount, kmean, ktimed, kflops, kbytes, kbound = timed[0]
+    if kbound == "mfma":
+        achieved, peak, unit = kflops / (kmean * 1e-3) / 1e12, MFMA_PEAK_TFLOPS, "TFLOP/s"
+    else:
+        achieved, peak, unit = kbytes / (kmean * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s"
     roofline = {
         "bound": kbound,
         "achieved": round(achieved, 3),
         "peak": peak,
-        "unit": "TFLOP/s" if kbound == "mfma" else "GB/s",
+        "unit": unit,
         "frac": round(achieved / peak, 5),
         "traffic": load_traffic(kname, spec.name),
         "kernel": kname,
         "launch_ms_mean": round(kmean, 5),
         "launches_per_step": kcount,
         "launches_timed": ktimed,
-        "work_per_launch": kwork,
+        "flops_per_launch": kflops,
+        "bytes_per_launch": kbytes,
     }
-    breakdown = {name: {"mean_ms": round(mean, 5), "per_step": count,
-                        "share_est": round(share / ms_per_step, 4)}
-                 for share, name, count, mean, _, _, _ in timed}
+    breakdown = {}
+    for share, name, count, mean, _, flops, nbytes, bound in timed:
+        rate = flops / (mean * 1e-3) / 1e12 if bound == "mfma" else nbytes / (mean * 1e-3) / 1e9
+        breakdown[name] = {"mean_ms": round(mean, 5), "per_step": count, "bound": bound,
+                           "achieved": round(rate, 2), "unit": "TFLOP/s" if bound == "mfma" else "GB/s",
+                           "share_est": round(share / ms_per_step, 4)}
 
     cpu = None
     if not args.no_cpu_baseline:

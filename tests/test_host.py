@@ -1,0 +1,234 @@
+"""Host-side contracts that need no GPU.
+
+The C-ABI library loads here and exports every entry point its header
+declares.  The candidate module keeps the reference's plugin contracts
+(transformer_benchmark/models.py, tests/test_models.py of the reference): CPU
+fallback op order, the packed Q/K/V state dict, mask classification and graph
+replay returning independent clones.  The rocprof summary tool parses the CSV
+layout rocprofv3 writes.
+"""
+
+import ctypes
+import json
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from tiktoktechjam2026track3_amd import native, profiling
+from tiktoktechjam2026track3_amd.cases import TransformerConfig
+from tiktoktechjam2026track3_amd.correctness import compare_outputs
+from tiktoktechjam2026track3_amd.models import (
+    BaselineTransformer,
+    UnsupportedShapeError,
+    UserOptimizedTransformer,
+    classify_mask,
+    copy_model_weights,
+)
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+# ------------------------------------------------------------------ C ABI ----
+
+def declared_entry_points():
+    text = (ROOT / "include" / "mi355x_encoder.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(enc_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_entry_point():
+    lib = ctypes.CDLL(str(native.LIBRARY_PATH))
+    names = declared_entry_points()
+    assert len(names) >= 10
+    for name in names:
+        assert hasattr(lib, name), f"{name} declared in the header but not exported"
+
+
+def test_binding_covers_the_header_exactly():
+    assert sorted(name for name, _, _ in native.SIGNATURES) == declared_entry_points()
+
+
+def test_library_reports_version_and_errors_without_a_gpu():
+    lib = native.load_library()
+    assert lib.enc_version() >> 16 == 1
+    # argument validation happens before any device call
+    rc = lib.enc_layernorm_bf16(None, None, None, None, 4, 256, 1e-5, None, None)
+    assert rc == native.ENC_ERR_INVALID
+    assert b"null" in lib.enc_last_error()
+    rc = lib.enc_linear_bf16(None, None, None, None, None, 4, 100, 64, 0, None, None)
+    assert rc in (native.ENC_ERR_INVALID, native.ENC_ERR_UNSUPPORTED)
+    assert lib.enc_encoder_workspace_bytes(1, 128, 512, 8, 2048) > 0
+    assert lib.enc_encoder_workspace_bytes(1, 128, 500, 8, 2048) == -1  # D % H != 0
+
+
+# -------------------------------------------------------- plugin contracts ----
+
+def _pair(config, seed):
+    torch.manual_seed(seed)
+    baseline = BaselineTransformer(config).eval()
+    optimized = UserOptimizedTransformer(config).eval()
+    copy_model_weights(baseline, optimized)
+    return baseline, optimized
+
+
+def test_cpu_candidate_is_bitwise_the_baseline_in_fp32():
+    """The CPU path runs the baseline's op sequence (reference
+    tests/test_models.py:53-67 pins the same property with torch.equal)."""
+    config = TransformerConfig(4, 8, 16, 4, 32, 1, True)
+    baseline, optimized = _pair(config, 4321)
+    x = torch.randn(4, 8, 16)
+    mask = torch.ones(4, 8, dtype=torch.bool)
+    mask[1, -3:] = False
+    x = x.masked_fill(~mask[..., None], 0)
+    with torch.inference_mode():
+        assert torch.equal(baseline(x, mask), optimized(x, mask))
+
+
+def test_cpu_candidate_with_padding_passes_reference_gate():
+    config = TransformerConfig(1, 128, 128, 4, 128, 2, True)
+    baseline, optimized = _pair(config, 1234)
+    x = torch.randn(1, 128, 128)
+    mask = torch.ones(1, 128, dtype=torch.bool)
+    mask[:, -32:] = False
+    x = x.masked_fill(~mask[..., None], 0)
+    with torch.inference_mode():
+        result = compare_outputs(baseline(x, mask), optimized(x, mask), rtol=0.02, atol=0.002)
+    assert result.passed
+    assert optimized._cuda_graph is None
+
+
+def test_legacy_qkv_state_dict_is_packed_q_then_k_then_v():
+    config = TransformerConfig(1, 8, 16, 4, 32, 1, False)
+    baseline, optimized = _pair(config, 7)
+    attn_b = baseline.layers[0].attention
+    attn_o = optimized.layers[0].attention
+    expected_w = torch.cat([attn_b.q_proj.weight, attn_b.k_proj.weight, attn_b.v_proj.weight])
+    expected_b = torch.cat([attn_b.q_proj.bias, attn_b.k_proj.bias, attn_b.v_proj.bias])
+    assert torch.equal(attn_o.qkv_proj.weight, expected_w)
+    assert torch.equal(attn_o.qkv_proj.bias, expected_b)
+
+
+def test_packed_state_dict_round_trips_strictly():
+    config = TransformerConfig(1, 8, 16, 4, 32, 2, False)
+    _, optimized = _pair(config, 8)
+    other = UserOptimizedTransformer(config)
+    other.load_state_dict(optimized.state_dict(), strict=True)
+    for (k1, v1), (k2, v2) in zip(optimized.state_dict().items(), other.state_dict().items()):
+        assert k1 == k2 and torch.equal(v1, v2)
+
+
+def test_incomplete_or_ambiguous_legacy_state_is_rejected():
+    config = TransformerConfig(1, 8, 16, 4, 32, 1, False)
+    baseline, _ = _pair(config, 9)
+    sd = baseline.state_dict()
+    incomplete = {k: v for k, v in sd.items() if "v_proj.bias" not in k}
+    with pytest.raises(RuntimeError, match="incomplete legacy"):
+        UserOptimizedTransformer(config).load_state_dict(incomplete)
+    ambiguous = dict(sd)
+    ambiguous["layers.0.attention.qkv_proj.weight"] = torch.zeros(48, 16)
+    with pytest.raises(RuntimeError, match="ambiguous"):
+        UserOptimizedTransformer(config).load_state_dict(ambiguous)
+
+
+def test_mask_classes():
+    assert classify_mask(torch.ones(2, 8, dtype=torch.bool)) == "all_true"
+    prefix = torch.arange(8)[None, :] < torch.tensor([[5], [8]])
+    assert classify_mask(prefix) == "prefix"
+    general = prefix.clone()
+    general[0, 1] = False
+    assert classify_mask(general) == "general"
+
+
+def test_mask_classification_tracks_mutation_and_inference_tensors():
+    config = TransformerConfig(1, 128, 128, 4, 128, 4, True)
+    optimized = UserOptimizedTransformer(config).eval()
+    mask = torch.ones(1, 128, dtype=torch.bool)
+    assert optimized._mask_is_all_true(mask)
+    mask[0, -1] = False
+    assert not optimized._mask_is_all_true(mask)
+    with torch.inference_mode():
+        inference_mask = torch.ones(1, 128, dtype=torch.bool)
+        assert optimized._mask_is_all_true(inference_mask)
+        inference_mask[0, -1] = False
+        assert not optimized._mask_is_all_true(inference_mask)
+
+
+def test_graph_replay_returns_independent_outputs():
+    """Replays hand back clones of the static output (reference
+    tests/test_models.py:666-691)."""
+    config = TransformerConfig(1, 8, 16, 4, 32, 1, True)
+    optimized = UserOptimizedTransformer(config).eval()
+    static_output = torch.zeros(1)
+
+    class FakeGraph:
+        def replay(self) -> None:
+            static_output.add_(1)
+
+    optimized._cuda_graph = FakeGraph()
+    optimized._cuda_graph_output = static_output
+    optimized._cuda_graph_signature = ("stable",)
+    optimized._cuda_graph_eligible = lambda _x, _mask: True
+    optimized._cuda_graph_live_signature = lambda _x, _mask, _kind: ("stable",)
+    x = torch.zeros(1, 8, 16)
+    mask = torch.ones(1, 8, dtype=torch.bool)
+    first = optimized(x, mask)
+    second = optimized(x, mask)
+    assert first is not second
+    assert first.item() == 1.0 and second.item() == 2.0
+
+
+def test_native_path_rejects_shapes_the_kernels_do_not_cover():
+    config = TransformerConfig(1, 8, 128, 4, 128, 1, False)  # head_dim 32
+    model = UserOptimizedTransformer(config)
+    with pytest.raises(UnsupportedShapeError, match="head_dim 32"):
+        model._check_native_supported(torch.zeros(1, 8, 128, dtype=torch.bfloat16))
+    with pytest.raises(UnsupportedShapeError, match="bfloat16"):
+        model._check_native_supported(torch.zeros(1, 8, 128))
+
+
+# --------------------------------------------------------------- profiling ----
+
+def _write_csv(path: Path, header, rows):
+    path.parent.mkdir(parents=True, exist_ok=True)
+    lines = [",".join(f'"{h}"' for h in header)]
+    for row in rows:
+        lines.append(",".join(f'"{v}"' if isinstance(v, str) else str(v) for v in row))
+    path.write_text("\n".join(lines) + "\n")
+
+
+def test_profiling_summary_scales_counters_by_the_copy_calibration(tmp_path):
+    stats_header = ["Name", "Calls", "TotalDurationNs", "AverageNs", "Percentage", "MinNs", "MaxNs", "StdDev"]
+    _write_csv(tmp_path / "trace" / "run_kernel_stats.csv", stats_header, [
+        ["void enc::(anonymous namespace)::gemm_big_kernel<256, 128>(unsigned short const*)", 4, 400.0, 100.0, 80.0, 90, 110, 1.0],
+        ["at::cuda::(anonymous namespace)::spin_kernel(long)", 1, 1e9, 1e9, 10.0, 1, 1, 0.0],
+        ["__amd_rocclr_copyBuffer", 2, 100.0, 50.0, 20.0, 40, 60, 1.0],
+    ])
+    pmc_header = ["Correlation_Id", "Dispatch_Id", "Agent_Id", "Queue_Id", "Process_Id", "Thread_Id", "Grid_Size",
+                  "Kernel_Id", "Kernel_Name", "Workgroup_Size", "LDS_Block_Size", "Scratch_Size", "VGPR_Count",
+                  "Accum_VGPR_Count", "SGPR_Count", "Counter_Name", "Counter_Value", "Start_Timestamp", "End_Timestamp"]
+    gemm = "void enc::(anonymous namespace)::gemm_big_kernel<256, 128>(unsigned short const*)"
+    for kind, counter, gemm_vals, copy_val in (("fetch", "FETCH_SIZE", (100.0, 300.0), 1024.0 * 8),
+                                               ("write", "WRITE_SIZE", (50.0, 50.0), 1024.0 * 16)):
+        rows = [[i, i, "Agent 1", 1, 1, 1, 256, 1, gemm, 256, 0, 0, 64, 0, 32, counter, v, 0, 1]
+                for i, v in enumerate(gemm_vals)]
+        rows.append([9, 9, "Agent 1", 1, 1, 1, 256, 2, "__amd_rocclr_copyBuffer", 256, 0, 0, 8, 0, 8, counter, copy_val, 0, 1])
+        rows.append([10, 10, "Agent 1", 1, 1, 1, 256, 2, "__amd_rocclr_copyBuffer", 256, 0, 0, 8, 0, 8, counter, 3.0, 0, 1])
+        _write_csv(tmp_path / kind / "run_counter_collection.csv", pmc_header, rows)
+    out = tmp_path / "summary.md"
+    traffic = tmp_path / "traffic.json"
+    rc = profiling.main([
+        "--trace", str(tmp_path / "trace"), "--fetch", str(tmp_path / "fetch"), "--write", str(tmp_path / "write"),
+        "--copy-mib", "16", "--workload", "cX", "--label", "gemm=gemm_big_kernel<256, 128>",
+        "--algorithmic-bytes", "gemm=1000000", "--out", str(out), "--traffic", str(traffic),
+    ])
+    assert rc == 0
+    table = json.loads(traffic.read_text())["gemm@cX"]
+    # fetch: 16 MiB copy read 8192 units -> 2048 bytes per unit; mean 200 units
+    assert table["fetched"] == 200 * 2048
+    # write: 16 MiB copy wrote 16384 units -> 1024 bytes per unit; mean 50 units
+    assert table["written"] == 50 * 1024
+    assert table["bytes_per_launch"] == 200 * 2048 + 50 * 1024
+    text = out.read_text()
+    assert "gemm_big_kernel<256, 128>" in text and "spin_kernel" not in text

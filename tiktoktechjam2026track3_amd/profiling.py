@@ -1,0 +1,220 @@
+"""rocprofv3 evidence for the encoder kernels: per-kernel time and HBM traffic.
+
+Reads the CSV files ``rocprofv3 --output-format csv`` writes:
+
+* ``<run>_kernel_stats.csv`` of a ``--kernel-trace --stats`` run: calls and
+  average / total duration per kernel;
+* ``<run>_counter_collection.csv`` of a ``--pmc FETCH_SIZE`` run and of a
+  ``--pmc WRITE_SIZE`` run (one counter set per run): KiB per dispatch.
+
+Counter values are scaled by what the same counter reads for a device copy of
+known size in the same process (``bench.py --copy-calibration-mib N`` ends
+with one; it is the largest ``__amd_rocclr_copyBuffer`` dispatch), so the
+traffic figures are in bytes of HBM actually moved.
+
+    python -m tiktoktechjam2026track3_amd.profiling \\
+        --trace gpurun_out/trace_c2 --fetch gpurun_out/fetch_c2 --write gpurun_out/write_c2 \\
+        --copy-mib 256 --workload c2 --label ffn_out_residual='gemm_bf16_kernel<64, 64, 3' \\
+        --command "..." --out profiles/encoder_c2.md --traffic profiles/traffic.json
+
+writes a markdown summary and merges ``{"<label>@<workload>": {...}}`` entries
+into the traffic table ``bench.py`` reports as ``roofline.traffic``.
+
+This module only reads profiler output; it never loads the GPU library.
+"""
+
+from __future__ import annotations
+
+import argparse
+import csv
+import glob
+import json
+import os
+from collections import defaultdict
+from dataclasses import dataclass
+from typing import Dict, List, Optional, Sequence, Tuple
+
+COPY_KERNEL = "__amd_rocclr_copyBuffer"
+
+
+@dataclass
+class KernelStat:
+    name: str
+    calls: int
+    total_ns: float
+    average_ns: float
+    percentage: float
+
+
+def _find(directory: str, suffix: str) -> str:
+    matches = sorted(glob.glob(os.path.join(directory, "**", f"*{suffix}"), recursive=True))
+    if not matches:
+        raise FileNotFoundError(f"no *{suffix} under {directory}")
+    return matches[0]
+
+
+def short_name(name: str, limit: int = 72) -> str:
+    """Kernel name without namespaces and argument list, template kept,
+    cut to ``limit`` characters."""
+    name = name.replace("void ", "").replace("enc::(anonymous namespace)::", "")
+    depth = 0
+    for i, ch in enumerate(name):
+        if ch == "<":
+            depth += 1
+        elif ch == ">":
+            depth -= 1
+        elif ch == "(" and depth == 0:
+            name = name[:i]
+            break
+    return name if len(name) <= limit else name[: limit - 3] + "..."
+
+
+def read_kernel_stats(directory: str) -> List[KernelStat]:
+    path = _find(directory, "kernel_stats.csv")
+    out = []
+    with open(path, newline="") as fh:
+        for row in csv.DictReader(fh):
+            out.append(
+                KernelStat(
+                    name=row["Name"],
+                    calls=int(row["Calls"]),
+                    total_ns=float(row["TotalDurationNs"]),
+                    average_ns=float(row["AverageNs"]),
+                    percentage=float(row["Percentage"]),
+                )
+            )
+    return out
+
+
+def read_counter(directory: str, counter: str) -> Dict[str, List[float]]:
+    """Per kernel name, the counter's value (KiB) of every dispatch."""
+    path = _find(directory, "counter_collection.csv")
+    values: Dict[str, List[float]] = defaultdict(list)
+    with open(path, newline="") as fh:
+        for row in csv.DictReader(fh):
+            if row["Counter_Name"] == counter:
+                values[row["Kernel_Name"]].append(float(row["Counter_Value"]))
+    if not values:
+        raise ValueError(f"{path} holds no {counter} values")
+    return values
+
+
+def calibration(values: Dict[str, List[float]], copy_mib: int) -> float:
+    """Bytes per counter unit: known copy bytes over the largest copy dispatch."""
+    copies = values.get(COPY_KERNEL, [])
+    if not copies or max(copies) <= 0:
+        raise ValueError("no calibration copy dispatch found")
+    return copy_mib * 1024.0 * 1024.0 / max(copies)
+
+
+def match(names: Sequence[str], pattern: str) -> List[str]:
+    return [n for n in names if pattern in n]
+
+
+def traffic_for(pattern: str, fetch: Dict[str, List[float]], write: Dict[str, List[float]],
+                fetch_scale: float, write_scale: float) -> Tuple[float, float, int]:
+    """Mean fetched and written bytes per dispatch of the kernels matching pattern."""
+    names = match(list(fetch), pattern)
+    if not names:
+        raise ValueError(f"no profiled kernel matches {pattern!r}")
+    f_vals = [v for n in names for v in fetch[n]]
+    w_vals = [v for n in match(list(write), pattern) for v in write[n]]
+    fetched = sum(f_vals) / len(f_vals) * fetch_scale
+    written = (sum(w_vals) / len(w_vals) * write_scale) if w_vals else 0.0
+    return fetched, written, len(f_vals)
+
+
+def summarize(stats: List[KernelStat], top: int = 12) -> str:
+    lines = [
+        "| kernel | calls | avg (µs) | total (ms) | share |",
+        "|---|---:|---:|---:|---:|",
+    ]
+    for st in stats[:top]:
+        lines.append(
+            f"| `{short_name(st.name)}` | {st.calls} | {st.average_ns / 1e3:.2f} | "
+            f"{st.total_ns / 1e6:.3f} | {st.percentage:.1f}% |"
+        )
+    return "\n".join(lines)
+
+
+def main(argv: Optional[Sequence[str]] = None) -> int:
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--trace", required=True, help="output dir of the --kernel-trace --stats run")
+    p.add_argument("--fetch", help="output dir of the --pmc FETCH_SIZE run")
+    p.add_argument("--write", help="output dir of the --pmc WRITE_SIZE run")
+    p.add_argument("--copy-mib", type=int, default=0, help="size of bench.py's calibration copy")
+    p.add_argument("--workload", required=True)
+    p.add_argument("--label", action="append", default=[],
+                   help="LABEL=PATTERN: bench kernel label and a substring of its rocprof name")
+    p.add_argument("--algorithmic-bytes", action="append", default=[],
+                   help="LABEL=BYTES: algorithmic bytes per launch, for the ratio")
+    p.add_argument("--command", action="append", default=[], help="command lines that produced the runs")
+    p.add_argument("--title", default="")
+    p.add_argument("--out", required=True)
+    p.add_argument("--traffic", help="JSON traffic table to merge into")
+    p.add_argument("--exclude", action="append", default=["spin_kernel"],
+                   help="substring of kernels to leave out of the table (the bench's host-latency busy-wait)")
+    args = p.parse_args(argv)
+
+    stats = [s for s in read_kernel_stats(args.trace) if not any(x in s.name for x in args.exclude)]
+    total = sum(s.total_ns for s in stats) or 1.0
+    for s in stats:
+        s.percentage = 100.0 * s.total_ns / total
+    doc = [f"# {args.title or 'rocprofv3 kernel summary: ' + args.workload}", ""]
+    doc.append("Produced by (from the repository root on one MI355X, `cd /tmp && export TMPDIR=/tmp` first):")
+    doc.append("")
+    for c in args.command:
+        doc.append(f"    {c}")
+    doc.append("")
+    doc.append("Kernel time (kernel-trace run; share of all profiled kernel time):")
+    doc.append("")
+    doc.append(summarize(stats))
+    doc.append("")
+
+    algorithmic = dict(item.split("=", 1) for item in args.algorithmic_bytes)
+    if args.fetch and args.write and args.label:
+        fetch = read_counter(args.fetch, "FETCH_SIZE")
+        write = read_counter(args.write, "WRITE_SIZE")
+        fs = calibration(fetch, args.copy_mib)
+        ws = calibration(write, args.copy_mib)
+        doc.append(
+            f"HBM traffic per dispatch (PMC runs; FETCH_SIZE scaled by {fs / 1024:.4f} KiB per unit "
+            f"and WRITE_SIZE by {ws / 1024:.4f}, from a {args.copy_mib} MiB device copy in the same process):"
+        )
+        doc.append("")
+        doc.append("| kernel | dispatches | fetched (MB) | written (MB) | total (MB) | algorithmic (MB) | ratio |")
+        doc.append("|---|---:|---:|---:|---:|---:|---:|")
+        table = {}
+        if args.traffic and os.path.exists(args.traffic):
+            with open(args.traffic) as fh:
+                table = json.load(fh)
+        for item in args.label:
+            label, pattern = item.split("=", 1)
+            fetched, written, n = traffic_for(pattern, fetch, write, fs, ws)
+            alg = float(algorithmic[label]) if label in algorithmic else None
+            ratio = f"{(fetched + written) / alg:.2f}" if alg else "—"
+            alg_txt = f"{alg / 1e6:.3f}" if alg else "—"
+            doc.append(
+                f"| {label} (`{pattern}`) | {n} | {fetched / 1e6:.3f} | {written / 1e6:.3f} | "
+                f"{(fetched + written) / 1e6:.3f} | {alg_txt} | {ratio} |"
+            )
+            table[f"{label}@{args.workload}"] = {
+                "bytes_per_launch": round(fetched + written),
+                "fetched": round(fetched),
+                "written": round(written),
+                "kernel": pattern,
+                "dispatches": n,
+            }
+        if args.traffic:
+            with open(args.traffic, "w") as fh:
+                json.dump(table, fh, indent=1, sort_keys=True)
+                fh.write("\n")
+        doc.append("")
+    with open(args.out, "w") as fh:
+        fh.write("\n".join(doc))
+    print(args.out)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())
