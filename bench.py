@@ -315,8 +315,8 @@ def main(argv=None) -> int:
         "bytes_per_launch": kbytes,
     }
     breakdown = {}
-    for share, name, count, mean, _, flops, nbytes, bound in timed:
-        rate = flops / (mean * 1e-3) / 1e12 if bound == "mfma" else nbytes / (mean * 1e-3) / 1e9
+    for share, name, count, mean, _, k_flops, k_bytes, bound in timed:
+        rate = k_flops / (mean * 1e-3) / 1e12 if bound == "mfma" else k_bytes / (mean * 1e-3) / 1e9
         breakdown[name] = {"mean_ms": round(mean, 5), "per_step": count, "bound": bound,
                            "achieved": round(rate, 2), "unit": "TFLOP/s" if bound == "mfma" else "GB/s",
                            "share_est": round(share / ms_per_step, 4)}

@@ -10,6 +10,7 @@ from .encoder_oracle import (  # noqa: F401
     attention_rows,
     compare,
     encoder_forward,
+    encoder_forward_sequences,
     encoder_layer,
     final_norm,
     generate_case,

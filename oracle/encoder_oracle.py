@@ -18,6 +18,9 @@ Functions and the reference lines they restate:
                     row masking)
   final_norm        models.py:916-918
   encoder_forward   models.py:909-919
+  encoder_forward_sequences
+                    models.py:909-919 for a subset of the batch, Linear and
+                    LayerNorm on the whole batch (the reference's GEMM shapes)
   compare           correctness.py:63-67 strict OR rule
 
 Parity pinning (tests/test_oracle.py): every function above is checked against
@@ -152,6 +155,21 @@ def attention_rows(
     return torch.matmul(probs, v)
 
 
+def even_block_rows(seq_len: int, limit: int = ORACLE_ATTENTION_BLOCK_ROWS) -> int:
+    """Largest query-row block size <= limit that divides seq_len (at least
+    half of limit), else limit.  Equal blocks give every block the same
+    product shape, so the library accumulates each one the same way; a
+    ragged last block can be given a different K order (e.g. at S = 100000
+    with 1024-row blocks, the 672-row tail block's P.V product differs from
+    the others' in the last bit)."""
+    if seq_len <= limit:
+        return seq_len
+    for rows in range(limit, limit // 2 - 1, -1):
+        if seq_len % rows == 0:
+            return rows
+    return limit
+
+
 def _heads(t: torch.Tensor, num_heads: int) -> torch.Tensor:
     b, s, d = t.shape
     return t.view(b, s, num_heads, d // num_heads).transpose(1, 2).contiguous()
@@ -207,6 +225,64 @@ def encoder_layer(
     if row_mask is not None:
         y = y.masked_fill(~row_mask[..., None], 0)
     return y
+
+
+def encoder_forward_sequences(
+    sd: StateDict,
+    x: torch.Tensor,
+    sequences: Sequence[int],
+    causal: bool,
+    num_heads: int,
+    num_layers: int,
+    eps: float = 1e-5,
+    block_rows: Optional[int] = None,
+) -> torch.Tensor:
+    """The reference forward (no mask) evaluated for the listed sequences only,
+    with every Linear and LayerNorm run on the whole [B, S, D] batch exactly as
+    the reference runs them (models.py:30-33, 721-725: nn.Linear flattens the
+    batch into one [B*S, D] product, whose accumulation order the library picks
+    for that whole shape).  Attention, whose score tensor would not fit, is the
+    row-blocked restatement of models.py:55-70 for the listed sequences; the
+    other sequences' contexts are left zero, which changes nothing for the
+    listed ones because every Linear and LayerNorm row depends only on its own
+    input row.  Returns [len(sequences), S, D]."""
+    b, s, d = x.shape
+    hd = d // num_heads
+    scale = hd**-0.5
+    rows = torch.arange(s, device=x.device)
+    if block_rows is None:
+        block_rows = even_block_rows(s)
+    for layer in range(num_layers):
+        p = f"layers.{layer}."
+        a = f"{p}attention."
+        h = F.layer_norm(x, (d,), sd[p + "norm1.weight"], sd[p + "norm1.bias"], eps)
+        context = torch.zeros(b, s, d, device=x.device, dtype=x.dtype)
+        q_all = F.linear(h, sd[a + "q_proj.weight"], sd[a + "q_proj.bias"])
+        k_all = F.linear(h, sd[a + "k_proj.weight"], sd[a + "k_proj.bias"])
+        v_all = F.linear(h, sd[a + "v_proj.weight"], sd[a + "v_proj.bias"])
+        del h
+        for seq in sequences:
+            q = _heads(q_all[seq : seq + 1], num_heads)
+            k = _heads(k_all[seq : seq + 1], num_heads)
+            v = _heads(v_all[seq : seq + 1], num_heads)
+            ctx = torch.empty_like(q)
+            for start in range(0, s, block_rows):
+                stop = min(s, start + block_rows)
+                ctx[:, :, start:stop] = attention_rows(
+                    q[:, :, start:stop], k, v, scale, causal, None, rows[start:stop]
+                )
+            context[seq] = ctx.transpose(1, 2).reshape(s, d)
+            del q, k, v, ctx
+        del q_all, k_all, v_all
+        x = x + F.linear(context, sd[a + "out_proj.weight"], sd[a + "out_proj.bias"])
+        del context
+        h2 = F.layer_norm(x, (d,), sd[p + "norm2.weight"], sd[p + "norm2.bias"], eps)
+        hidden = F.gelu(F.linear(h2, sd[p + "ffn_in.weight"], sd[p + "ffn_in.bias"]), approximate="none")
+        del h2
+        x = x + F.linear(hidden, sd[p + "ffn_out.weight"], sd[p + "ffn_out.bias"])
+        del hidden
+    y = F.layer_norm(x, (d,), sd["final_norm.weight"], sd["final_norm.bias"], eps)
+    return y[list(sequences)]
 
 
 def final_norm(

@@ -248,3 +248,14 @@ def test_final_mask_is_what_zeroes_padded_rows():
     assert torch.all(y[~mask] == 0) and bool((y[mask] != 0).any())
     assert torch.allclose(unmasked[~mask], torch.full_like(unmasked[~mask], 0.25))  # the planted mistake shows
     assert torch.equal(unmasked[mask], y[mask])
+
+
+def test_sequence_subset_forward_equals_full_forward():
+    """encoder_forward_sequences (whole-batch Linear layers, attention for the
+    listed sequences only) gives the full forward's values on those sequences."""
+    b, s_len, d, h, f, layers = 3, 16, 32, 4, 64, 2
+    sd = eo.init_state_dict(d, h, f, layers, seed=5)
+    x, _ = eo.generate_case(b, s_len, d, CPU, torch.float32, 6, 0.0)
+    full = eo.encoder_forward(sd, x, None, False, h, layers, block_rows=4)
+    sub = eo.encoder_forward_sequences(sd, x, (0, 2), False, h, layers, block_rows=4)
+    torch.testing.assert_close(sub, full[[0, 2]], rtol=1e-5, atol=1e-6)
