@@ -1,0 +1,47 @@
+"""The CLI drop-in on the GPU: measurement configurations through the native
+forward, the accuracy gate of the reference, timing, roofline and the bounded
+candidate profile, written as a benchmarkctl-compatible schema 2 document."""
+
+import json
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+
+from tests.test_runner import benchmarkctl_summary
+
+pytestmark = pytest.mark.gpu
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def test_cli_encoder_configs_c2_c3_pass_the_gate_with_profile(tmp_path):
+    out = tmp_path / "result.json"
+    cmd = [sys.executable, "-u", str(ROOT / "torch_transformer_benchmark.py"), "--encoder-configs", "c2", "c3",
+           "--rtol", "1.6e-2", "--atol", "1e-2", "--accuracy-trials", "2", "--warmup", "3", "--repeats", "10",
+           "--benchmark-rounds", "2", "--profile-candidate", "--json-output", str(out)]
+    proc = subprocess.run(cmd, cwd=ROOT, capture_output=True, text=True, timeout=600)
+    print(proc.stdout[-3000:], proc.stderr[-2000:], flush=True)
+    assert proc.returncode == 0
+    doc = json.loads(out.read_text())
+    assert benchmarkctl_summary(doc) == {"mode": "official_matrix", "correctness_passed": True}
+    assert doc["requested_case_ids"] == [2, 3]
+    for case in doc["cases"]:
+        assert case["status"] == "succeeded"
+        assert case["accuracy"]["failed_elements"] == 0
+        roof = case["performance"]["roofline"]
+        assert 0 < roof["fraction_of_bf16_mfma_peak"] < 1
+        profile = case["candidate_profile"]
+        assert profile["profiled_replays"] == 3 and len(profile["replay_wall_time"]["samples_ms"]) == 3
+    assert doc["environment"]["compute_units"] > 0
+
+
+def test_cli_official_case_with_unsupported_head_dim_is_an_execution_failure(tmp_path):
+    out = tmp_path / "official.json"
+    cmd = [sys.executable, "-u", str(ROOT / "torch_transformer_benchmark.py"), "--official-cases", "2",
+           "--accuracy-trials", "1", "--json-output", str(out)]
+    proc = subprocess.run(cmd, cwd=ROOT, capture_output=True, text=True, timeout=600)
+    assert proc.returncode == 3, proc.stdout[-2000:] + proc.stderr[-2000:]
+    doc = json.loads(out.read_text())
+    benchmarkctl_summary(doc)
+    assert doc["cases"][0]["failure_category"] == "unsupported_shape"

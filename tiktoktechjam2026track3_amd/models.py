@@ -36,11 +36,25 @@ import torch.nn.functional as F
 from .cases import TransformerConfig
 
 # Upper bound on the bytes of score temporaries one baseline attention call may
-# hold at once; above it the baseline walks query-row blocks.
+# hold at once; above it the baseline walks sequences and query-row blocks.
 SCORE_MEMORY_BUDGET_BYTES = 16 * 1024**3
 # Bytes per score element the baseline keeps alive at peak (bf16 scores, the
 # scaled/masked copies, fp32 softmax input and output, bf16 probabilities).
 SCORE_BYTES_PER_ELEMENT = 16
+# Preferred query rows per block when the baseline walks one sequence at a time.
+BLOCK_ROWS_LIMIT = 1024
+
+
+def even_row_block(seq_len: int, limit: int) -> int:
+    """Largest row-block size <= limit dividing seq_len (down to limit / 2),
+    else limit.  Equal blocks give every block's products the same shape, so
+    the BLAS library accumulates all of them the same way."""
+    if seq_len <= limit:
+        return seq_len
+    for rows in range(limit, limit // 2 - 1, -1):
+        if seq_len % rows == 0:
+            return rows
+    return limit
 
 # Token count up to which the candidate captures a HIP graph (launch-bound shapes).
 GRAPH_MAX_TOKENS = 4096
@@ -110,14 +124,20 @@ class BaselineSelfAttention(nn.Module):
         per_row = b * h * s * SCORE_BYTES_PER_ELEMENT
         if per_row * s <= SCORE_MEMORY_BUDGET_BYTES:
             return _attention_core(q, k, v, self.scale, causal, valid_token_mask, 0, s)
-        # Row-blocked evaluation of the identical per-row math.
-        block = max(1, SCORE_MEMORY_BUDGET_BYTES // per_row)
+        # The identical per-row math, one sequence and one block of query rows
+        # at a time (softmax is row-local, sequences are independent); this is
+        # what lets shapes whose score tensor cannot exist (S = 100000) run.
+        limit = max(1, min(BLOCK_ROWS_LIMIT, 4 * SCORE_MEMORY_BUDGET_BYTES // (per_row // b)))
+        block = even_row_block(s, limit)
         out = torch.empty_like(q)
-        for start in range(0, s, block):
-            stop = min(s, start + block)
-            out[..., start:stop, :] = _attention_core(
-                q, k, v, self.scale, causal, valid_token_mask, start, stop
-            )
+        for seq in range(b):
+            mask = None if valid_token_mask is None else valid_token_mask[seq : seq + 1]
+            qs, ks, vs = q[seq : seq + 1], k[seq : seq + 1], v[seq : seq + 1]
+            for start in range(0, s, block):
+                stop = min(s, start + block)
+                out[seq : seq + 1, :, start:stop, :] = _attention_core(
+                    qs, ks, vs, self.scale, causal, mask, start, stop
+                )
         return out
 
     def forward(
