@@ -566,6 +566,169 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
   }
 }
 
+// ---------------------------------------------------------------------------
+// Skinny kernel for few rows (M <= 256): latency, not MFMA throughput, bounds
+// these products, so the work is cut into many small independent pieces.
+// v_mfma_f32_16x16x16_bf16 keeps the 16-deep K grouping of the 32x32x16 tiles
+// above (the same accumulation as the library's kernels).  Lane layout:
+//   A operand : row l%16, k = 4*(l/16) + j      (j = 0..3, 8 contiguous bytes)
+//   B operand : col l%16, k = 4*(l/16) + j      (a W row, 8 contiguous bytes)
+//   C/D       : col l%16, row = 4*(l/16) + j
+// A and W stream through a two-stage LDS ring in K slices of 256 (512 bytes a
+// row) with direct global->LDS loads: one instruction moves two whole rows, so
+// global reads are fully coalesced.  Inside a row the 16-byte chunk c sits in
+// slot c ^ (row & 15), so the 16 rows one fragment read touches fall in
+// distinct bank groups.
+//   SPLIT == 1: 4 wavefronts, workgroup tile 16 x 64, wavefront w owns
+//               columns 16w .. 16w+15 over the full K range in order.
+//   SPLIT  > 1: SPLIT wavefronts, workgroup tile 16 x 16; K is cut into
+//               CW-wide chunks and wavefront p accumulates chunks p, p+SPLIT,
+//               ... (the library's split order); the partials meet in LDS and
+//               are added in order before the bias.
+constexpr int kSkinnyMaxRows = 256;  // products with at most this many rows use it
+constexpr int kSkinnyKS = 256;       // K elements per LDS stage
+constexpr int kSkinnyRow = kSkinnyKS;  // LDS row length, elements
+
+template <int EPI>
+__device__ __forceinline__ void store_one(const GemmEpilogueArgs& ep, int N, int row, int col, float acc,
+                                          float bias) {
+  if constexpr (EPI == kEpiQkvHeadMajor) {
+    const float y = acc + bias;
+    const int D = ep.d_model, hd = ep.head_dim, S = ep.seq_len;
+    const int which = col / D;
+    const int rem = col - which * D;
+    const int h = rem / hd;
+    const int d = rem - h * hd;
+    const int b = row / S;
+    const int s = row - b * S;
+    const int64_t bh = static_cast<int64_t>(b) * ep.num_heads + h;
+    if (which < 2) {
+      bf16_t* dst = which == 0 ? ep.q : ep.k;
+      dst[(bh * S + s) * hd + d] = f32_to_bf16(y);
+    } else {
+      ep.v_t[(bh * hd + d) * ep.ld_vt + s] = f32_to_bf16(y);
+    }
+  } else {
+    store_row_major<EPI>(ep, N, row, col, acc, bias);
+  }
+}
+
+template <int EPI, int SPLIT, int CW>
+__global__ void __launch_bounds__(256)
+gemm_skinny_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int M, int N, int K,
+                   GemmEpilogueArgs ep) {
+  constexpr int kWaves = SPLIT == 1 ? 4 : SPLIT;
+  constexpr int kBN = SPLIT == 1 ? 64 : 16;
+  constexpr int kRows = 16 + kBN;                       // LDS rows per stage (A then W)
+  constexpr int kStage = kRows * kSkinnyRow;            // elements per stage
+  constexpr int kLoads = kRows / 2 / kWaves;            // 2-row load instructions per wavefront
+  constexpr int kStepsPerChunk = CW / 16;
+  static_assert(kRows % (2 * kWaves) == 0, "load split");
+  static_assert(SPLIT == 1 || (CW % 16 == 0 && kSkinnyKS % (CW * SPLIT) == 0), "chunk width");
+  __shared__ __attribute__((aligned(16))) bf16_t smem[2 * kStage];
+  __shared__ float red[SPLIT > 1 ? SPLIT : 1][64][4];
+
+  const int tiles_m = (M + 15) / 16;
+  // consecutive workgroups share a W column panel (the larger operand)
+  const int tm = blockIdx.x % tiles_m;
+  const int tn = blockIdx.x / tiles_m;
+  const int m0 = tm * 16;
+  const int n0 = tn * kBN;
+  const int lane = threadIdx.x % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int l16 = lane & 15;
+  const int g = lane >> 4;
+
+  // Load instruction j of wavefront w fills LDS rows 2(kWaves j + w) and +1;
+  // lane L writes slot L%32 of row +L/32, holding chunk (L%32) ^ (row & 15).
+  const int ld_half = lane >> 5;
+  auto issue_stage = [&](int stage, int k0) {
+    bf16_t* base = smem + stage * kStage;
+#pragma unroll
+    for (int j = 0; j < kLoads; ++j) {
+      const int r0 = 2 * (kWaves * j + wave);
+      const int r = r0 + ld_half;
+      const int chunk = (lane & 31) ^ (r & 15);
+      const bf16_t* src;
+      if (r < 16) {
+        src = A + static_cast<int64_t>(min(m0 + r, M - 1)) * K;  // rows past M: a valid row, never stored
+      } else {
+        src = W + static_cast<int64_t>(n0 + r - 16) * K;
+      }
+      __builtin_amdgcn_global_load_lds(src + k0 + chunk * 8, base + r0 * kSkinnyRow, 16, 0, 0);
+    }
+  };
+  // fragment (8 bytes) of LDS row r at K-step s of the stage: chunk 2s + g/2
+  auto frag = [&](int stage, int r, int s) {
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    const int chunk = 2 * s + (g >> 1);
+    const bf16_t* p = smem + stage * kStage + r * kSkinnyRow + ((chunk ^ (r & 15)) << 3) + 4 * (g & 1);
+    return *reinterpret_cast<const s16x4*>(p);
+  };
+
+  const int wrow = 16 + (SPLIT == 1 ? wave * 16 : 0) + l16;  // this lane's W row in the stage
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  const int nst = K / kSkinnyKS;
+  issue_stage(0, 0);
+  if (nst > 1) issue_stage(1, kSkinnyKS);
+  for (int st = 0; st < nst; ++st) {
+    const int buf = st & 1;
+    // the other stage's loads may still be in flight
+    if (st + 1 < nst) {
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(kLoads));
+    } else {
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    }
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < kSkinnyKS / 16; ++s) {
+      bool mine = true;
+      if constexpr (SPLIT > 1) mine = ((s / kStepsPerChunk) % SPLIT) == wave;
+      if (mine) acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(frag(buf, l16, s), frag(buf, wrow, s), acc, 0, 0, 0);
+    }
+    __syncthreads();  // every wavefront is done with this stage
+    if (st + 2 < nst) issue_stage(buf, (st + 2) * kSkinnyKS);
+  }
+
+  const int col = n0 + (SPLIT == 1 ? wave * 16 : 0) + l16;
+  if constexpr (SPLIT > 1) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) red[wave][lane][j] = acc[j];
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float sum = red[0][lane][j];
+#pragma unroll
+      for (int p = 1; p < SPLIT; ++p) sum += red[p][lane][j];
+      acc[j] = sum;
+    }
+  }
+  const float bias = bf16_to_f32(ep.bias[col]);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r = m0 + 4 * g + j;
+    if (r < M) store_one<EPI>(ep, N, r, col, acc[j], bias);
+  }
+}
+
+template <int SPLIT, int CW>
+hipError_t launch_skinny(const bf16_t* A, const bf16_t* W, int M, int N, int K, int epi,
+                         const GemmEpilogueArgs& ep, hipStream_t st) {
+  constexpr int kWaves = SPLIT == 1 ? 4 : SPLIT;
+  constexpr int kBN = SPLIT == 1 ? 64 : 16;
+  const dim3 grid(((M + 15) / 16) * (N / kBN)), block(kWaves * kWave);
+  switch (epi) {
+    case kEpiBias: hipLaunchKernelGGL((gemm_skinny_kernel<kEpiBias, SPLIT, CW>), grid, block, 0, st, A, W, M, N, K, ep); break;
+    case kEpiBiasGelu: hipLaunchKernelGGL((gemm_skinny_kernel<kEpiBiasGelu, SPLIT, CW>), grid, block, 0, st, A, W, M, N, K, ep); break;
+    case kEpiResidualKeep: hipLaunchKernelGGL((gemm_skinny_kernel<kEpiResidualKeep, SPLIT, CW>), grid, block, 0, st, A, W, M, N, K, ep); break;
+    case kEpiResidualZero: hipLaunchKernelGGL((gemm_skinny_kernel<kEpiResidualZero, SPLIT, CW>), grid, block, 0, st, A, W, M, N, K, ep); break;
+    case kEpiQkvHeadMajor: hipLaunchKernelGGL((gemm_skinny_kernel<kEpiQkvHeadMajor, SPLIT, CW>), grid, block, 0, st, A, W, M, N, K, ep); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 struct TileShape {
   int bm, bn;
   int blocks_per_cu;  // resident workgroups per CU (LDS / register bound)
@@ -720,6 +883,15 @@ hipError_t gemm_bf16(const bf16_t* A, const bf16_t* W, int64_t M, int64_t N, int
   const int m = static_cast<int>(M), n = static_cast<int>(N), k = static_cast<int>(K);
   int split, chunk;
   gemm_split_plan(M, N, K, &split, &chunk);
+  const bool aligned16 = reinterpret_cast<uintptr_t>(A) % 16 == 0 && reinterpret_cast<uintptr_t>(W) % 16 == 0;
+  // whole LDS stages, each holding whole rounds of the split's chunks
+  const bool whole = K % kSkinnyKS == 0 && kSkinnyKS % (chunk * split) == 0;
+  if (M <= kSkinnyMaxRows && aligned16 && whole) {
+    if (split == 1) return launch_skinny<1, 16>(A, W, m, n, k, epi, ep, stream);
+    if (split == 4 && chunk == 32) return launch_skinny<4, 32>(A, W, m, n, k, epi, ep, stream);
+    if (split == 4 && chunk == 64) return launch_skinny<4, 64>(A, W, m, n, k, epi, ep, stream);
+    if (split == 2 && chunk == 128) return launch_skinny<2, 128>(A, W, m, n, k, epi, ep, stream);
+  }
   if (split == 4 && chunk == 32) return launch_split<4, 32>(A, W, m, n, k, epi, ep, stream);
   if (split == 4 && chunk == 64) return launch_split<4, 64>(A, W, m, n, k, epi, ep, stream);
   if (split == 2 && chunk == 128) return launch_split<2, 128>(A, W, m, n, k, epi, ep, stream);
