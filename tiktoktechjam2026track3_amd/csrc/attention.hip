@@ -86,7 +86,10 @@ __device__ __forceinline__ int tile_key(int kb32, int r, int h) {
   return 32 * kb32 + 16 * (i >> 1) + 8 * h + 4 * (i & 1) + j;
 }
 
-template <int NW, bool CAUSAL, int MASK, bool POW2_SCALE, bool BLOCK_ORDER>
+// RES > 0: short rows (at most RES tiles): every K/V tile is loaded into LDS
+// once and the three sweeps read them from there, with no further loads or
+// barriers.  RES == 0: the two-stage ring streams the tiles for each sweep.
+template <int NW, bool CAUSAL, int MASK, bool POW2_SCALE, bool BLOCK_ORDER, int RES>
 __global__ void __launch_bounds__(NW * kWave)
 attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
                      const bf16_t* __restrict__ Vt, bf16_t* __restrict__ ctx, int H, int S,
@@ -94,9 +97,14 @@ attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg
                      const int32_t* __restrict__ kv_len, const uint8_t* __restrict__ key_mask) {
   constexpr int kThreads = NW * kWave;
   constexpr int kBQ = NW * 32;
-  __shared__ __attribute__((aligned(16))) bf16_t sK[2][kTileElems];
-  __shared__ __attribute__((aligned(16))) bf16_t sV[2][kTileElems];
-  __shared__ uint8_t sM[2][kBKV];
+  // K, V^T and key-mask tiles live in dynamic LDS sized at launch
+  // (attn_lds_bytes): a static __shared__ array whose size depends on a
+  // template parameter loses the kernel's host launch stub in this compiler.
+  constexpr int kBufs = RES > 0 ? RES : 2;
+  extern __shared__ __attribute__((aligned(16))) bf16_t attn_lds[];
+  bf16_t (*sK)[kTileElems] = reinterpret_cast<bf16_t (*)[kTileElems]>(attn_lds);
+  bf16_t (*sV)[kTileElems] = reinterpret_cast<bf16_t (*)[kTileElems]>(attn_lds + kBufs * kTileElems);
+  uint8_t (*sM)[kBKV] = reinterpret_cast<uint8_t (*)[kBKV]>(attn_lds + 2 * kBufs * kTileElems);
 
   // Block -> (batch*head, query tile).  Non-causal: MI355X hands consecutive
   // workgroups to its 8 XCDs round-robin; the id is remapped so each XCD walks
@@ -222,16 +230,28 @@ attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg
 
   // Runs body(buf, tile) over nkb tiles in the order seq(0), seq(1), ...,
   // double-buffered: the loads of the next tile overlap the current body.
+  // With resident tiles the body reads tile t from buffer t.
+  bool resident = false;
   auto sweep = [&](auto seq, bool with_v, auto body) {
-    if (nkb > 0) issue_tile(0, seq(0), with_v);
-    __builtin_amdgcn_s_waitcnt(kWaitVm0);
-    __syncthreads();
-    for (int it = 0; it < nkb; ++it) {
-      const int cur = it & 1;
-      if (it + 1 < nkb) issue_tile(cur ^ 1, seq(it + 1), with_v);
-      body(cur, seq(it));
+    if (RES > 0) {
+      if (!resident) {
+        for (int t = 0; t < nkb; ++t) issue_tile(t, t, true);
+        __builtin_amdgcn_s_waitcnt(kWaitVm0);
+        __syncthreads();
+        resident = true;
+      }
+      for (int it = 0; it < nkb; ++it) body(seq(it), seq(it));
+    } else {
+      if (nkb > 0) issue_tile(0, seq(0), with_v);
       __builtin_amdgcn_s_waitcnt(kWaitVm0);
       __syncthreads();
+      for (int it = 0; it < nkb; ++it) {
+        const int cur = it & 1;
+        if (it + 1 < nkb) issue_tile(cur ^ 1, seq(it + 1), with_v);
+        body(cur, seq(it));
+        __builtin_amdgcn_s_waitcnt(kWaitVm0);
+        __syncthreads();
+      }
     }
   };
 
@@ -543,16 +563,30 @@ attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg
   }
 }
 
-template <int NW, bool CAUSAL, int MASK, bool POW2, bool BLOCK_ORDER>
+// LDS bytes of one attention workgroup: K and V^T tiles plus key-mask bytes
+constexpr size_t attn_lds_bytes(int res) {
+  return static_cast<size_t>(res > 0 ? res : 2) * (2 * kTileElems * sizeof(bf16_t) + kBKV);
+}
+
+template <int NW, bool CAUSAL, int MASK, bool POW2, bool BLOCK_ORDER, int RES = 0>
 hipError_t launch_attn(const bf16_t* q, const bf16_t* k, const bf16_t* vt, bf16_t* ctx, int B,
                        int H, int S, float scale, const int32_t* kv_len, const uint8_t* key_mask,
                        hipStream_t st) {
   constexpr int kBQ = NW * 32;
+  constexpr size_t kLds = attn_lds_bytes(RES);
   const int nqb = (S + kBQ - 1) / kBQ;
   const dim3 grid(static_cast<uint32_t>(B) * H * nqb);
   const int ld_vt = static_cast<int>(vt_stride(S));
-  hipLaunchKernelGGL((attn_fwd_hd64_kernel<NW, CAUSAL, MASK, POW2, BLOCK_ORDER>), grid, dim3(NW * kWave),
-                     0, st, q, k, vt, ctx, H, S, ld_vt, nqb, scale, kv_len, key_mask);
+  auto kernel = attn_fwd_hd64_kernel<NW, CAUSAL, MASK, POW2, BLOCK_ORDER, RES>;
+  if constexpr (kLds > 64 * 1024) {
+    // above 64 KiB of dynamic LDS the kernel has to opt in (once per process)
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                       static_cast<int>(kLds));
+    if (attr != hipSuccess) return attr;
+  }
+  hipLaunchKernelGGL(kernel, grid, dim3(NW * kWave), kLds, st, q, k, vt, ctx, H, S, ld_vt, nqb, scale, kv_len,
+                     key_mask);
   return hipGetLastError();
 }
 
@@ -564,9 +598,19 @@ hipError_t dispatch_order(const bf16_t* q, const bf16_t* k, const bf16_t* vt, bf
     return launch_attn<4, CAUSAL, MASK, POW2, true>(q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
   // Small problems use one-wavefront workgroups (32 queries) so more of the
   // 256 CUs get work; larger ones share each K/V tile among 4 wavefronts.
+  // Rows of at most 256 keys keep every tile resident in LDS.
   const int64_t groups128 = static_cast<int64_t>(B) * H * ((S + 127) / 128);
-  if (groups128 < 512)
+  if (groups128 < 512) {
+    if (S <= 2 * kBKV)
+      return launch_attn<1, CAUSAL, MASK, POW2, false, 2>(q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
+    if (S <= 4 * kBKV)
+      return launch_attn<1, CAUSAL, MASK, POW2, false, 4>(q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
     return launch_attn<1, CAUSAL, MASK, POW2, false>(q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
+  }
+  if (S <= 2 * kBKV)
+    return launch_attn<4, CAUSAL, MASK, POW2, false, 2>(q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
+  if (S <= 4 * kBKV)
+    return launch_attn<4, CAUSAL, MASK, POW2, false, 4>(q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
   return launch_attn<4, CAUSAL, MASK, POW2, false>(q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
 }
 
