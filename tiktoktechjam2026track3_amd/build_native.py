@@ -95,8 +95,25 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     if verbose:
         print(" ".join(link))
     _run(link)
+    _check_launch_stubs(tmp)
     os.replace(tmp, LIBRARY_PATH)
     return LIBRARY_PATH
+
+
+def _check_launch_stubs(path: Path) -> None:
+    """Fail the build when a kernel's host-side launch stub is missing.
+
+    Some kernel template bodies make clang's host pass drop the stub without a
+    diagnostic; the library then links but cannot be loaded.  ``nm`` lists
+    such stubs as undefined symbols.
+    """
+    nm = shutil.which("nm")
+    if nm is None:
+        return
+    proc = subprocess.run([nm, "-D", "--undefined-only", str(path)], capture_output=True, text=True)
+    missing = [line.split()[-1] for line in proc.stdout.splitlines() if "__device_stub__" in line]
+    if missing:
+        raise RuntimeError(f"{path.name}: {len(missing)} kernel launch stub(s) missing, e.g. {missing[0]}")
 
 
 if __name__ == "__main__":

@@ -68,6 +68,20 @@ __device__ __forceinline__ float gelu_erf(float x) {
   return 0.5f * x * (1.0f + erff(x * 0.70710678118654752440f));
 }
 
+// s_waitcnt immediate (gfx9 encoding): wait until at most `vm` vector-memory
+// and `lgkm` LDS operations of this wavefront are outstanding.
+constexpr int waitcnt_imm(int vm, int lgkm) {
+  return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | ((lgkm & 15) << 8);
+}
+
+// Workgroup barrier for global->LDS rings.  __syncthreads() is also a
+// workgroup release/acquire fence, which the compiler implements with
+// s_waitcnt vmcnt(0): that drains every prefetched stage still in flight.
+// Here the caller first waits (s_waitcnt) for exactly the loads and LDS reads
+// it needs finished; the memory clobber keeps the compiler from moving LDS
+// accesses across the barrier.
+__device__ __forceinline__ void ring_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);

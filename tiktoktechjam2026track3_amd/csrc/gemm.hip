@@ -306,9 +306,26 @@ gemm_bf16_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int
 // rows of 8 head channels and V^T columns of 8 sequence positions.
 constexpr int kLdsLimitBytes = 160 * 1024;
 
-// s_waitcnt immediate that waits until at most n vector-memory operations are
-// outstanding (expcnt and lgkmcnt left at their no-wait maxima; gfx9 layout).
-constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+// Instruction order inside one K step: MFMA q is followed by the LDS reads
+// and global loads with indices in [q * per, (q + 1) * per), so the reads and
+// loads issue early, while the MFMA pipe is busy, instead of in a burst that
+// the wavefront then waits on.
+template <int MFMA, int READS, int LOADS>
+__device__ __forceinline__ void interleave() {
+  constexpr int kReadsPer = (READS + MFMA - 1) / MFMA;
+  constexpr int kLoadsPer = (LOADS + MFMA - 1) / MFMA;
+#pragma unroll
+  for (int q = 0; q < MFMA; ++q) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+#pragma unroll
+    for (int r = q * kReadsPer; r < (q + 1) * kReadsPer && r < READS; ++r)
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+#pragma unroll
+    for (int l = q * kLoadsPer; l < (q + 1) * kLoadsPer && l < LOADS; ++l)
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // global load
+  }
+}
 
 template <int BM, int BN, int BK, int NS>
 struct BigTile {
@@ -376,7 +393,7 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
 
   const int tid = threadIdx.x;
   const int lane = tid % kWave;
-  const int wave = tid / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int wm = wave >> 1;
   const int wn = wave & 1;
   const int l32 = lane & 31;
@@ -388,24 +405,33 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
   // first row (32-bit); the bases are uniform.
   const int lrow = lane / T::kChunks;
   const int gcol = ((lane % T::kChunks) ^ T::swz(lrow)) * 8;
-  const bf16_t* a_tile = A + static_cast<int64_t>(m0) * K;
-  const bf16_t* w_tile = W + static_cast<int64_t>(n0) * K;
+  // Each load instruction reads [uniform base + per-lane 32-bit byte offset];
+  // the offsets do not change along K (the compiler hoists them), only the
+  // bases do.  (They are not precomputed into an array: a local array
+  // captured by this lambda makes clang's host pass drop the kernel's launch
+  // stub.)
+  const char* a_tile = reinterpret_cast<const char*>(A + static_cast<int64_t>(m0) * K);
+  const char* w_tile = reinterpret_cast<const char*>(W + static_cast<int64_t>(n0) * K);
   const int a_rows_left = M - 1 - m0;  // rows past M re-load the last row, never stored
   auto issue_loads = [&](int stage, int k0) {
     bf16_t* sa = smem + stage * T::kStage;
     bf16_t* sb = sa + BM * BK;
+    const char* ab = a_tile + 2 * k0;
+    const char* wb = w_tile + 2 * k0;
 #pragma unroll
     for (int j = 0; j < T::kLoadsA; ++j) {
       const int row = T::kRowsPerLoad * (4 * j + wave);
-      const int ra = min(row + lrow, a_rows_left);
-      __builtin_amdgcn_global_load_lds(a_tile + k0 + (ra * K + gcol), sa + row * BK, 16, 0, 0);
+      const uint32_t off = static_cast<uint32_t>(min(row + lrow, a_rows_left) * K + gcol) * 2u;
+      __builtin_amdgcn_global_load_lds(ab + off, sa + row * BK, 16, 0, 0);
     }
 #pragma unroll
     for (int j = 0; j < T::kLoadsB; ++j) {
       const int row = T::kRowsPerLoad * (4 * j + wave);
-      __builtin_amdgcn_global_load_lds(w_tile + k0 + ((row + lrow) * K + gcol), sb + row * BK, 16, 0, 0);
+      const uint32_t off = static_cast<uint32_t>((row + lrow) * K + gcol) * 2u;
+      __builtin_amdgcn_global_load_lds(wb + off, sb + row * BK, 16, 0, 0);
     }
   };
+
 
   f32x16 acc[RM][RN];
 #pragma unroll
@@ -428,60 +454,89 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
 #pragma unroll
     for (int j = 0; j < RN; ++j) bf[j] = *reinterpret_cast<const bf16x8*>(st + b_off + j * 32 * BK + slot);
   };
-  // Wait until K block `ready` has landed, given that blocks up to `issued`
-  // were requested (each block is T::kLoads instructions of this thread).
-  auto wait_block = [&](int ready, int issued) {
-    const int later = min(issued - ready, NS - 2);
+  // Wait until at most `later` K blocks of this thread's loads are still in
+  // flight and its LDS reads are done (the stage it read is refilled after
+  // the barrier that follows).
+  auto wait_loads = [&](int later) {
     if (later <= 0) {
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+      __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
     } else if (later == 1) {
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(T::kLoads));
+      __builtin_amdgcn_s_waitcnt(waitcnt_imm(T::kLoads, 0));
+    } else if (later == 2) {
+      __builtin_amdgcn_s_waitcnt(waitcnt_imm(2 * T::kLoads, 0));
     } else {
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(T::kLoads * (NS - 2 > 1 ? 2 : 1)));
+      __builtin_amdgcn_s_waitcnt(waitcnt_imm(3 * T::kLoads, 0));
     }
   };
-  static_assert(NS <= 4, "wait_block covers at most two later blocks");
+  static_assert(NS <= 4 && 3 * T::kLoads < 64, "vmcnt range");
+  auto mfma_step = [&](const bf16x8 (&a)[RM], const bf16x8 (&b)[RN]) {
+#pragma unroll
+    for (int i = 0; i < RM; ++i)
+#pragma unroll
+      for (int j = 0; j < RN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+  };
 
   const int KT = K / BK;
-  int issued = -1;
-  for (int p = 0; p < NS - 1 && p < KT; ++p) {
-    issue_loads(p, p * BK);
-    issued = p;
-  }
-  wait_block(0, issued);
-  __syncthreads();
+  const int prologue = min(NS, KT);
+  for (int p = 0; p < prologue; ++p) issue_loads(p, p * BK);
+  wait_loads(prologue - 1);
+  ring_barrier();
   bf16x8 af[RM], bf[RN];
   read_frags(0, 0, af, bf);
-  int stage = 0;
-  for (int kt = 0; kt < KT; ++kt) {
-    if (kt + NS - 1 < KT) {
-      int ls = stage + NS - 1;
-      if (ls >= NS) ls -= NS;
-      issue_loads(ls, (kt + NS - 1) * BK);
-      issued = kt + NS - 1;
-    }
+
+  // K block kt (in LDS stage `stage`): steps 0 .. KS-2 multiply while the
+  // next step's fragments are read.  Then one barrier: block kt + 1 has landed
+  // for every wavefront and nobody reads stage `stage` any more.  The last
+  // step multiplies while block kt + NS is requested into that stage and step
+  // 0 of block kt + 1 is read, so no LDS or memory latency is left exposed
+  // between blocks.
+  constexpr int KS = BK / 16;
+  // (A plain lambda with constant arguments at each call: a generic lambda
+  // here makes clang drop the kernel's host-side launch stub.)
+  auto k_block = [&](int kt, int stage, int later, bool load, bool next) __attribute__((always_inline)) {
 #pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
+    for (int ks = 0; ks + 1 < KS; ++ks) {
       bf16x8 an[RM], bn[RN];
-      if (ks + 1 < BK / 16) read_frags(stage, ks + 1, an, bn);
+      read_frags(stage, ks + 1, an, bn);
+      mfma_step(af, bf);
+      interleave<RM * RN, RM + RN, 0>();
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int i = 0; i < RM; ++i)
+      for (int i = 0; i < RM; ++i) af[i] = an[i];
 #pragma unroll
-        for (int j = 0; j < RN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
-      if (ks + 1 < BK / 16) {
-#pragma unroll
-        for (int i = 0; i < RM; ++i) af[i] = an[i];
-#pragma unroll
-        for (int j = 0; j < RN; ++j) bf[j] = bn[j];
-      }
+      for (int j = 0; j < RN; ++j) bf[j] = bn[j];
     }
-    // block kt + 1 landed for every wave; nobody reads `stage` any more
-    if (kt + 1 < KT) wait_block(kt + 1, issued);
-    __syncthreads();
+    wait_loads(next ? later : 0);  // K blocks requested after block kt + 1; the epilogue reuses the ring
+    ring_barrier();
+    if (load) issue_loads(stage, (kt + NS) * BK);
+    bf16x8 an[RM], bn[RN];
+    if (next) read_frags(stage + 1 == NS ? 0 : stage + 1, 0, an, bn);
+    mfma_step(af, bf);
+    if (load) {
+      interleave<RM * RN, RM + RN, T::kLoads>();
+    } else if (next) {
+      interleave<RM * RN, RM + RN, 0>();
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (next) {
+#pragma unroll
+      for (int i = 0; i < RM; ++i) af[i] = an[i];
+#pragma unroll
+      for (int j = 0; j < RN; ++j) bf[j] = bn[j];
+    }
+  };
+  int stage = 0;
+  int kt = 0;
+  for (; kt + NS < KT; ++kt) {
+    k_block(kt, stage, NS - 2, true, true);
     stage = stage + 1 == NS ? 0 : stage + 1;
-    if (kt + 1 < KT) read_frags(stage, 0, af, bf);
   }
+  for (; kt + 1 < KT; ++kt) {
+    k_block(kt, stage, KT - 2 - kt, false, true);
+    stage = stage + 1 == NS ? 0 : stage + 1;
+  }
+  k_block(kt, stage, 0, false, false);
 
   // ---- epilogue: y = bf16(acc + bias) into LDS, then 8 outputs per thread ----
   bf16_t* sc = smem;  // every wave passed the last barrier: the stages are free
@@ -675,18 +730,19 @@ gemm_skinny_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, i
     const int buf = st & 1;
     // the other stage's loads may still be in flight
     if (st + 1 < nst) {
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(kLoads));
+      __builtin_amdgcn_s_waitcnt(waitcnt_imm(kLoads, 0));
     } else {
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+      __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
     }
-    __syncthreads();
+    ring_barrier();
 #pragma unroll
     for (int s = 0; s < kSkinnyKS / 16; ++s) {
       bool mine = true;
       if constexpr (SPLIT > 1) mine = ((s / kStepsPerChunk) % SPLIT) == wave;
       if (mine) acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(frag(buf, l16, s), frag(buf, wrow, s), acc, 0, 0, 0);
     }
-    __syncthreads();  // every wavefront is done with this stage
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 0));
+    ring_barrier();  // every wavefront is done reading this stage
     if (st + 2 < nst) issue_stage(buf, (st + 2) * kSkinnyKS);
   }
 
