@@ -35,9 +35,8 @@ constexpr int kThreads = 256;
 constexpr int kNumXcd = 8;
 constexpr int kGroupM = 8;
 
-__device__ __forceinline__ void map_tile(int tiles_m, int tiles_n, int* tm, int* tn) {
+__device__ __forceinline__ void map_tile(int tiles_m, int tiles_n, int pid, int* tm, int* tn) {
   const int num = tiles_m * tiles_n;
-  int pid = blockIdx.x;
   // XCD remap: workgroups pid = x + 8*slot run on XCD x.
   {
     const int xcd = pid % kNumXcd;
@@ -164,7 +163,7 @@ gemm_bf16_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int
   const int tiles_m = (M + BM - 1) / BM;
   const int tiles_n = N / BN;
   int tm, tn;
-  map_tile(tiles_m, tiles_n, &tm, &tn);
+  map_tile(tiles_m, tiles_n, blockIdx.x, &tm, &tn);
   const int m0 = tm * BM;
   const int n0 = tn * BN;
 
@@ -387,7 +386,7 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
   const int tiles_m = (M + BM - 1) / BM;
   const int tiles_n = N / BN;
   int tm, tn;
-  map_tile(tiles_m, tiles_n, &tm, &tn);
+  map_tile(tiles_m, tiles_n, blockIdx.x, &tm, &tn);
   const int m0 = tm * BM;
   const int n0 = tn * BN;
 
@@ -408,30 +407,11 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
   // Each load instruction reads [uniform base + per-lane 32-bit byte offset];
   // the offsets do not change along K (the compiler hoists them), only the
   // bases do.  (They are not precomputed into an array: a local array
-  // captured by this lambda makes clang's host pass drop the kernel's launch
-  // stub.)
+  // captured by the loading lambda makes clang's host pass drop the kernel's
+  // launch stub.)
   const char* a_tile = reinterpret_cast<const char*>(A + static_cast<int64_t>(m0) * K);
   const char* w_tile = reinterpret_cast<const char*>(W + static_cast<int64_t>(n0) * K);
   const int a_rows_left = M - 1 - m0;  // rows past M re-load the last row, never stored
-  auto issue_loads = [&](int stage, int k0) {
-    bf16_t* sa = smem + stage * T::kStage;
-    bf16_t* sb = sa + BM * BK;
-    const char* ab = a_tile + 2 * k0;
-    const char* wb = w_tile + 2 * k0;
-#pragma unroll
-    for (int j = 0; j < T::kLoadsA; ++j) {
-      const int row = T::kRowsPerLoad * (4 * j + wave);
-      const uint32_t off = static_cast<uint32_t>(min(row + lrow, a_rows_left) * K + gcol) * 2u;
-      __builtin_amdgcn_global_load_lds(ab + off, sa + row * BK, 16, 0, 0);
-    }
-#pragma unroll
-    for (int j = 0; j < T::kLoadsB; ++j) {
-      const int row = T::kRowsPerLoad * (4 * j + wave);
-      const uint32_t off = static_cast<uint32_t>((row + lrow) * K + gcol) * 2u;
-      __builtin_amdgcn_global_load_lds(wb + off, sb + row * BK, 16, 0, 0);
-    }
-  };
-
 
   f32x16 acc[RM][RN];
 #pragma unroll
@@ -454,21 +434,43 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
 #pragma unroll
     for (int j = 0; j < RN; ++j) bf[j] = *reinterpret_cast<const bf16x8*>(st + b_off + j * 32 * BK + slot);
   };
-  // Wait until at most `later` K blocks of this thread's loads are still in
-  // flight and its LDS reads are done (the stage it read is refilled after
-  // the barrier that follows).
-  auto wait_loads = [&](int later) {
-    if (later <= 0) {
-      __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
-    } else if (later == 1) {
-      __builtin_amdgcn_s_waitcnt(waitcnt_imm(T::kLoads, 0));
-    } else if (later == 2) {
-      __builtin_amdgcn_s_waitcnt(waitcnt_imm(2 * T::kLoads, 0));
-    } else {
-      __builtin_amdgcn_s_waitcnt(waitcnt_imm(3 * T::kLoads, 0));
+  constexpr int KS = BK / 16;              // 16-wide K steps per block
+  constexpr int kPer = T::kLoads / KS;     // load instructions issued per step
+  static_assert(T::kLoads % KS == 0, "a block's loads split evenly over its steps");
+  // Part `part` of a block's loads: instructions [part * kPer, (part + 1) * kPer)
+  // of the list (A rows, then W rows).
+  // (The global loads are written out here rather than in helper lambdas: a
+  // device builtin in a lambda called from another lambda makes clang's host
+  // pass drop the kernel's launch stub.)
+  auto issue_part = [&](int stage, int k0, int part) {
+    bf16_t* sa = smem + stage * T::kStage;
+#pragma unroll
+    for (int q = 0; q < T::kLoads; ++q) {
+      if (q < part * kPer || q >= (part + 1) * kPer) continue;
+      const bool is_a = q < T::kLoadsA;
+      const int row = T::kRowsPerLoad * (4 * (is_a ? q : q - T::kLoadsA) + wave);
+      const uint32_t off = is_a ? static_cast<uint32_t>(min(row + lrow, a_rows_left) * K + gcol) * 2u
+                                : static_cast<uint32_t>((row + lrow) * K + gcol) * 2u;
+      __builtin_amdgcn_global_load_lds((is_a ? a_tile : w_tile) + 2 * k0 + off,
+                                       sa + (is_a ? 0 : BM * BK) + row * BK, 16, 0, 0);
     }
   };
-  static_assert(NS <= 4 && 3 * T::kLoads < 64, "vmcnt range");
+  // Wait until at most n of this thread's load instructions are in flight and
+  // its LDS reads are done (n is one of the counts the K loop uses; anything
+  // else waits for everything).
+  constexpr int kSteadyLater = (NS - 2) * T::kLoads - kPer;
+  static_assert(NS >= 3 && NS <= 4 && kSteadyLater >= 0 && 2 * T::kLoads < 64, "vmcnt range");
+  auto wait_vm = [&](int n) {
+    if (n == kSteadyLater) {
+      __builtin_amdgcn_s_waitcnt(waitcnt_imm(kSteadyLater, 0));
+    } else if (n == T::kLoads) {
+      __builtin_amdgcn_s_waitcnt(waitcnt_imm(T::kLoads, 0));
+    } else if (n == 2 * T::kLoads) {
+      __builtin_amdgcn_s_waitcnt(waitcnt_imm(2 * T::kLoads, 0));
+    } else {
+      __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
+    }
+  };
   auto mfma_step = [&](const bf16x8 (&a)[RM], const bf16x8 (&b)[RN]) {
 #pragma unroll
     for (int i = 0; i < RM; ++i)
@@ -477,44 +479,55 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
   };
 
+  // Prologue: blocks 0 .. NS-2 in full; block NS-1 loads during block 0.
   const int KT = K / BK;
-  const int prologue = min(NS, KT);
-  for (int p = 0; p < prologue; ++p) issue_loads(p, p * BK);
-  wait_loads(prologue - 1);
+  const int prologue = min(NS - 1, KT);
+  for (int p = 0; p < prologue; ++p)
+#pragma unroll
+    for (int part = 0; part < KS; ++part) issue_part(p, p * BK, part);
+  wait_vm((prologue - 1) * T::kLoads);
   ring_barrier();
   bf16x8 af[RM], bf[RN];
   read_frags(0, 0, af, bf);
 
-  // K block kt (in LDS stage `stage`): steps 0 .. KS-2 multiply while the
-  // next step's fragments are read.  Then one barrier: block kt + 1 has landed
-  // for every wavefront and nobody reads stage `stage` any more.  The last
-  // step multiplies while block kt + NS is requested into that stage and step
-  // 0 of block kt + 1 is read, so no LDS or memory latency is left exposed
-  // between blocks.
-  constexpr int KS = BK / 16;
-  // (A plain lambda with constant arguments at each call: a generic lambda
-  // here makes clang drop the kernel's host-side launch stub.)
+  // K block kt (in LDS stage `stage`).  Every step multiplies while the next
+  // step's fragments are read and one part of block kt + NS - 1 is requested
+  // into the stage block kt - 1 freed, so the loads are spread over the
+  // block instead of bunched.  Before the last step comes the one barrier:
+  // block kt + 1 has landed for every wavefront and nobody reads stage `stage`
+  // any more; the last step then reads step 0 of block kt + 1, so no LDS or
+  // memory latency is left exposed between blocks.
+  // (A plain lambda called with constant flags: a generic lambda makes clang
+  // drop the kernel's host-side launch stub, and runtime flags would merge
+  // differently scheduled MFMA results and double the accumulator registers.)
   auto k_block = [&](int kt, int stage, int later, bool load, bool next) __attribute__((always_inline)) {
+    const int lstage = stage == 0 ? NS - 1 : stage - 1;  // stage of block kt + NS - 1
+    const int lk0 = (kt + NS - 1) * BK;
 #pragma unroll
     for (int ks = 0; ks + 1 < KS; ++ks) {
       bf16x8 an[RM], bn[RN];
+      if (load) issue_part(lstage, lk0, ks);
       read_frags(stage, ks + 1, an, bn);
       mfma_step(af, bf);
-      interleave<RM * RN, RM + RN, 0>();
+      if (load) {
+        interleave<RM * RN, RM + RN, kPer>();
+      } else {
+        interleave<RM * RN, RM + RN, 0>();
+      }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < RM; ++i) af[i] = an[i];
 #pragma unroll
       for (int j = 0; j < RN; ++j) bf[j] = bn[j];
     }
-    wait_loads(next ? later : 0);  // K blocks requested after block kt + 1; the epilogue reuses the ring
+    wait_vm(next ? later : 0);  // loads requested after block kt + 1; the epilogue reuses the ring
     ring_barrier();
-    if (load) issue_loads(stage, (kt + NS) * BK);
     bf16x8 an[RM], bn[RN];
+    if (load) issue_part(lstage, lk0, KS - 1);
     if (next) read_frags(stage + 1 == NS ? 0 : stage + 1, 0, an, bn);
     mfma_step(af, bf);
     if (load) {
-      interleave<RM * RN, RM + RN, T::kLoads>();
+      interleave<RM * RN, RM + RN, kPer>();
     } else if (next) {
       interleave<RM * RN, RM + RN, 0>();
     }
@@ -528,12 +541,12 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
   };
   int stage = 0;
   int kt = 0;
-  for (; kt + NS < KT; ++kt) {
-    k_block(kt, stage, NS - 2, true, true);
+  for (; kt + NS - 1 < KT; ++kt) {
+    k_block(kt, stage, kSteadyLater, true, true);
     stage = stage + 1 == NS ? 0 : stage + 1;
   }
   for (; kt + 1 < KT; ++kt) {
-    k_block(kt, stage, KT - 2 - kt, false, true);
+    k_block(kt, stage, (KT - 2 - kt) * T::kLoads, false, true);
     stage = stage + 1 == NS ? 0 : stage + 1;
   }
   k_block(kt, stage, 0, false, false);
@@ -861,19 +874,25 @@ hipError_t launch_big(const bf16_t* A, const bf16_t* W, int M, int N, int K, int
 // Tile of the large-tile kernel for this shape, or 0 when the small-tile
 // kernel should run: the operands must be 16-byte aligned (16-byte loads per
 // lane), the residual / outputs too (16-byte epilogue stores), and the tile
-// count should fill the 256 CUs.
+// count should fill the device's CUs.
 int pick_big_tile(int64_t M, int64_t N, const bf16_t* A, const bf16_t* W, const GemmEpilogueArgs& ep,
-                  bool ep_is_gelu) {
+                  bool ep_is_gelu, int num_cus) {
   auto al = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
   if (!al(A) || !al(W) || !al(ep.out) || !al(ep.residual) || !al(ep.q) || !al(ep.k) || !al(ep.v_t)) return 0;
   if (M < 1024) return 0;
   // The erf GELU epilogue is long dependent VALU work; with two resident
   // 256x128 tiles per CU one tile's epilogue overlaps the other's MFMA loop.
   if (ep_is_gelu && N % 128 == 0) return 256129;
-  const int64_t t256 = ((M + 255) / 256) * (N / 256);
-  if (N % 256 == 0 && t256 >= 256) return 256256;
+  // Whole rounds of tiles over the CUs times the tile's work, over its
+  // measured per-tile efficiency (256x128 tiles run ~10% below 256x256).
+  auto cost = [&](int bm, int bn, double eff) {
+    const int64_t tiles = ((M + bm - 1) / bm) * (N / bn);
+    const int64_t rounds = (tiles + num_cus - 1) / num_cus;
+    return static_cast<double>(rounds) * bm * bn / eff;
+  };
   const int64_t t256x128 = ((M + 255) / 256) * (N / 128);
-  if (N % 128 == 0 && t256x128 >= 256) return 256128;
+  if (N % 256 == 0 && cost(256, 256, 1.0) <= cost(256, 128, 0.9)) return 256256;
+  if (N % 128 == 0 && t256x128 >= num_cus) return 256128;
   if (N % 128 == 0) return 128128;
   return 0;
 }
@@ -951,7 +970,7 @@ hipError_t gemm_bf16(const bf16_t* A, const bf16_t* W, int64_t M, int64_t N, int
   if (split == 4 && chunk == 32) return launch_split<4, 32>(A, W, m, n, k, epi, ep, stream);
   if (split == 4 && chunk == 64) return launch_split<4, 64>(A, W, m, n, k, epi, ep, stream);
   if (split == 2 && chunk == 128) return launch_split<2, 128>(A, W, m, n, k, epi, ep, stream);
-  switch (pick_big_tile(M, N, A, W, ep, epi == kEpiBiasGelu)) {
+  switch (pick_big_tile(M, N, A, W, ep, epi == kEpiBiasGelu, num_cus)) {
     case 256129: return launch_big<256, 128, 32, 3, 2>(A, W, m, n, k, epi, ep, stream);
     case 256256: return launch_big<256, 256, 32, 4>(A, W, m, n, k, epi, ep, stream);
     case 256128: return launch_big<256, 128, 64, 3>(A, W, m, n, k, epi, ep, stream);
