@@ -228,11 +228,15 @@ attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg
     }
   };
 
-  // Runs body(buf, tile) over nkb tiles in the order seq(0), seq(1), ...,
-  // double-buffered: the loads of the next tile overlap the current body.
-  // With resident tiles the body reads tile t from buffer t.
+  // Runs body(buf, tile) over the first `active` of the nkb tiles in the
+  // order seq(0), seq(1), ..., double-buffered: the loads of the next tile
+  // overlap the current body.  The remaining tiles (a causal wavefront's
+  // future) only take part in the loads and barriers the other wavefronts
+  // need; keeping them out of the body's loop (rather than skipping the body
+  // per tile) keeps the accumulators free of per-tile register copies.  With
+  // resident tiles the body reads tile t from buffer t.
   bool resident = false;
-  auto sweep = [&](auto seq, bool with_v, auto body) {
+  auto sweep = [&](auto seq, bool with_v, int active, auto body) {
     if (RES > 0) {
       if (!resident) {
         for (int t = 0; t < nkb; ++t) issue_tile(t, t, true);
@@ -240,15 +244,21 @@ attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg
         __syncthreads();
         resident = true;
       }
-      for (int it = 0; it < nkb; ++it) body(seq(it), seq(it));
+      for (int it = 0; it < active; ++it) body(seq(it), seq(it));
     } else {
       if (nkb > 0) issue_tile(0, seq(0), with_v);
       __builtin_amdgcn_s_waitcnt(kWaitVm0);
       __syncthreads();
-      for (int it = 0; it < nkb; ++it) {
+      int it = 0;
+      for (; it < active; ++it) {
         const int cur = it & 1;
         if (it + 1 < nkb) issue_tile(cur ^ 1, seq(it + 1), with_v);
         body(cur, seq(it));
+        __builtin_amdgcn_s_waitcnt(kWaitVm0);
+        __syncthreads();
+      }
+      for (; it < nkb; ++it) {
+        if (it + 1 < nkb) issue_tile((it & 1) ^ 1, seq(it + 1), with_v);
         __builtin_amdgcn_s_waitcnt(kWaitVm0);
         __syncthreads();
       }
@@ -257,6 +267,9 @@ attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg
 
   const int wq_first = q0 + wave * 32;
   const int wq_last = wq_first + 31;
+  // tiles of the natural order this wavefront multiplies (causal: those with
+  // a key <= its last query)
+  const int active = CAUSAL ? min(nkb, wq_last / kBKV + 1) : nkb;
 
   // Raw fp32 dot products of the 64-key tile in LDS buffer `buf`.
   auto tile_dots = [&](int buf, f32x16 (&s)[2]) {
@@ -329,9 +342,8 @@ attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg
   // max (and, for the short-row regime, min) of the raw dot products of the
   // allowed keys; the bf16 score of the max is formed once afterwards.
   float mx = -INFINITY, mn = INFINITY;
-  sweep(natural, false, [&](int buf, int kb) {
+  sweep(natural, false, active, [&](int buf, int kb) {
     const int k0 = kb * kBKV;
-    if (CAUSAL && k0 > wq_last) return;
     f32x16 s[2];
     tile_dots(buf, s);
     if (tile_needs_mask(k0)) {
@@ -380,9 +392,8 @@ attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg
       part[0][r] = 0.f;
       part[1][r] = 0.f;
     }
-    sweep(natural, false, [&](int buf, int kb) {
+    sweep(natural, false, active, [&](int buf, int kb) {
       const int k0 = kb * kBKV;
-      if (CAUSAL && k0 > wq_last) return;
       f32x16 s[2];
       tile_gaps(buf, k0, row_max, raw_max_bf, true, s);
 #pragma unroll
@@ -466,7 +477,7 @@ attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg
         warp_sum[7] = ws;
       }
     };
-    sweep(resmajor, false, [&](int buf, int kb) {
+    sweep(resmajor, false, nkb, [&](int buf, int kb) {
       const int k0 = kb * kBKV;
       const int r = kb & 31;
       while (cur_res < r) finish_residue();  // uniform
@@ -501,9 +512,8 @@ attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg
     o[0][r] = 0.f;
     o[1][r] = 0.f;
   }
-  sweep(natural, true, [&](int buf, int kb) {
+  sweep(natural, true, active, [&](int buf, int kb) {
     const int k0 = kb * kBKV;
-    if (CAUSAL && k0 > wq_last) return;
     f32x16 s[2];
     tile_gaps(buf, k0, row_max, raw_max_bf, !BLOCK_ORDER, s);
     bf16x8 pf[4];
