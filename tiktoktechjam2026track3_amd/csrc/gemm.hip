@@ -697,9 +697,17 @@ gemm_skinny_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, i
   __shared__ float red[SPLIT > 1 ? SPLIT : 1][64][4];
 
   const int tiles_m = (M + 15) / 16;
-  // consecutive workgroups share a W column panel (the larger operand)
-  const int tm = blockIdx.x % tiles_m;
-  const int tn = blockIdx.x / tiles_m;
+  // Tiles of one W column panel (the larger operand) are consecutive ids, and
+  // each XCD (workgroups are dealt to the 8 XCDs round-robin) takes a
+  // contiguous run of ids, so a panel is fetched into one XCD's L2 only.
+  int id;
+  {
+    const int pid = blockIdx.x, num = gridDim.x;
+    const int xcd = pid % kNumXcd, slot = pid / kNumXcd;
+    id = xcd * (num / kNumXcd) + min(xcd, num % kNumXcd) + slot;
+  }
+  const int tm = id % tiles_m;
+  const int tn = id / tiles_m;
   const int m0 = tm * 16;
   const int n0 = tn * kBN;
   const int lane = threadIdx.x % kWave;
