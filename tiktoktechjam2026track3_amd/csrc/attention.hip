@@ -304,9 +304,8 @@ attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg
   // rn(s - max) = scale * rn(bf16(q.k) - bf16(max raw dot)), so the scale
   // multiplies the difference (or folds into the exp2 multiplier below).
   // gap_scaled selects whether the returned g carries the scale.
-  auto tile_gaps = [&](int buf, int k0, float row_max, float raw_max_bf, bool gap_scaled,
-                       f32x16 (&s)[2]) {
-    tile_dots(buf, s);
+  auto dots_to_gaps = [&](int buf, int k0, float row_max, float raw_max_bf, bool gap_scaled,
+                          f32x16 (&s)[2]) {
 #pragma unroll
     for (int kb32 = 0; kb32 < 2; ++kb32) {
 #pragma unroll
@@ -336,15 +335,30 @@ attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg
           s[kb32][r] = key_ok(buf, k0, tile_key(kb32, r, lhi)) ? s[kb32][r] : -INFINITY;
     }
   };
+  auto tile_gaps = [&](int buf, int k0, float row_max, float raw_max_bf, bool gap_scaled,
+                       f32x16 (&s)[2]) {
+    tile_dots(buf, s);
+    dots_to_gaps(buf, k0, row_max, raw_max_bf, gap_scaled, s);
+  };
   auto natural = [](int it) { return it; };
+  // Rows of at most two tiles (RES == 2) keep each tile's values in registers
+  // across the sweeps: the dot products of sweep A become the gaps and then
+  // the weights e of sweep B, and sweep C reuses those e (the same values it
+  // would recompute), so every score's exponential is evaluated once.
+  constexpr bool kCache = RES == 2;
+  f32x16 cache[kCache ? 2 : 1][2];
+  auto load_resident = [&]() {
+    for (int t = 0; t < nkb; ++t) issue_tile(t, t, true);
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    __syncthreads();
+  };
 
   // ============================ sweep A: row max ============================
   // max (and, for the short-row regime, min) of the raw dot products of the
   // allowed keys; the bf16 score of the max is formed once afterwards.
   float mx = -INFINITY, mn = INFINITY;
-  sweep(natural, false, active, [&](int buf, int kb) {
+  auto max_body = [&](int buf, int kb, f32x16 (&s)[2]) {
     const int k0 = kb * kBKV;
-    f32x16 s[2];
     tile_dots(buf, s);
     if (tile_needs_mask(k0)) {
 #pragma unroll
@@ -363,7 +377,18 @@ attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg
         if constexpr (!BLOCK_ORDER) mn = fminf(mn, fminf(fminf(s[0][r], s[0][r + 1]), fminf(s[1][r], s[1][r + 1])));
       }
     }
-  });
+  };
+  if constexpr (kCache) {
+    load_resident();
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+      if (t < active) max_body(t, t, cache[t]);
+  } else {
+    sweep(natural, false, active, [&](int buf, int kb) {
+      f32x16 s[2];
+      max_body(buf, kb, s);
+    });
+  }
   mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
   auto to_score = [&](float raw) {
     const float rq = round_bf16(raw);
@@ -392,15 +417,30 @@ attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg
       part[0][r] = 0.f;
       part[1][r] = 0.f;
     }
-    sweep(natural, false, active, [&](int buf, int kb) {
-      const int k0 = kb * kBKV;
-      f32x16 s[2];
-      tile_gaps(buf, k0, row_max, raw_max_bf, true, s);
+    if constexpr (kCache) {
 #pragma unroll
-      for (int kb32 = 0; kb32 < 2; ++kb32)
+      for (int t = 0; t < 2; ++t) {
+        if (t >= active) continue;
+        dots_to_gaps(t, t * kBKV, row_max, raw_max_bf, true, cache[t]);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) part[kb32][r] += expf_nonpos(s[kb32][r]);
-    });
+        for (int kb32 = 0; kb32 < 2; ++kb32)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            cache[t][kb32][r] = expf_nonpos(cache[t][kb32][r]);
+            part[kb32][r] += cache[t][kb32][r];
+          }
+      }
+    } else {
+      sweep(natural, false, active, [&](int buf, int kb) {
+        const int k0 = kb * kBKV;
+        f32x16 s[2];
+        tile_gaps(buf, k0, row_max, raw_max_bf, true, s);
+#pragma unroll
+        for (int kb32 = 0; kb32 < 2; ++kb32)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) part[kb32][r] += expf_nonpos(s[kb32][r]);
+      });
+    }
     // 64-lane butterfly; lam bits: 5 = kb32, 4 = i>>1 (reg bit 3), 3 = lane half,
     // 2 = i&1 (reg bit 2), 1..0 = j (reg bits 1..0)
     float a[16];
@@ -512,17 +552,16 @@ attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg
     o[0][r] = 0.f;
     o[1][r] = 0.f;
   }
-  sweep(natural, true, active, [&](int buf, int kb) {
-    const int k0 = kb * kBKV;
-    f32x16 s[2];
-    tile_gaps(buf, k0, row_max, raw_max_bf, !BLOCK_ORDER, s);
+  // s holds the gaps, or (have_e) the weights e themselves
+  auto pv_body = [&](int buf, f32x16 (&s)[2], bool have_e) {
     bf16x8 pf[4];
     if (BLOCK_ORDER || !slow_div) {
 #pragma unroll
       for (int kb32 = 0; kb32 < 2; ++kb32) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const float e = BLOCK_ORDER ? __builtin_amdgcn_exp2f(s[kb32][r] * c_exp) : expf_nonpos(s[kb32][r]);
+          const float e = have_e ? s[kb32][r]
+                          : BLOCK_ORDER ? __builtin_amdgcn_exp2f(s[kb32][r] * c_exp) : expf_nonpos(s[kb32][r]);
           float p;
           if constexpr (BLOCK_ORDER) {
             p = e * inv_sum;
@@ -538,7 +577,7 @@ attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg
       for (int kb32 = 0; kb32 < 2; ++kb32) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const float e = expf_nonpos(s[kb32][r]);
+          const float e = have_e ? s[kb32][r] : expf_nonpos(s[kb32][r]);
           pf[kb32 * 2 + (r >> 3)][r & 7] = static_cast<__bf16>(e / row_sum);
         }
       }
@@ -551,7 +590,18 @@ attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg
         o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[kk], o[db], 0, 0, 0);
       }
     }
-  });
+  };
+  if constexpr (kCache) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+      if (t < active) pv_body(t, cache[t], true);
+  } else {
+    sweep(natural, true, active, [&](int buf, int kb) {
+      f32x16 s[2];
+      tile_gaps(buf, kb * kBKV, row_max, raw_max_bf, !BLOCK_ORDER, s);
+      pv_body(buf, s, false);
+    });
+  }
 
   // ---- write context[b, qrow, h*64 + d] = bf16(O) ----
   if (qrow < S) {
