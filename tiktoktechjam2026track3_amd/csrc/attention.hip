@@ -229,14 +229,14 @@ attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg
   };
 
   // Runs body(buf, tile) over the first `active` of the nkb tiles in the
-  // order seq(0), seq(1), ..., double-buffered: the loads of the next tile
-  // overlap the current body.  The remaining tiles (a causal wavefront's
-  // future) only take part in the loads and barriers the other wavefronts
-  // need; keeping them out of the body's loop (rather than skipping the body
-  // per tile) keeps the accumulators free of per-tile register copies.  With
-  // resident tiles the body reads tile t from buffer t.
+  // order 0, next(0), next(next(0)), ..., double-buffered: the loads of the
+  // next tile overlap the current body.  The remaining tiles (a causal
+  // wavefront's future) only take part in the loads and barriers the other
+  // wavefronts need; keeping them out of the body's loop (rather than skipping
+  // the body per tile) keeps the accumulators free of per-tile register
+  // copies.  With resident tiles the body reads tile t from buffer t.
   bool resident = false;
-  auto sweep = [&](auto seq, bool with_v, int active, auto body) {
+  auto sweep = [&](auto next, bool with_v, int active, auto body) {
     if (RES > 0) {
       if (!resident) {
         for (int t = 0; t < nkb; ++t) issue_tile(t, t, true);
@@ -244,23 +244,29 @@ attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg
         __syncthreads();
         resident = true;
       }
-      for (int it = 0; it < active; ++it) body(seq(it), seq(it));
+      int tile = 0;
+      for (int it = 0; it < active; ++it, tile = next(tile)) body(tile, tile);
     } else {
-      if (nkb > 0) issue_tile(0, seq(0), with_v);
+      int tile = 0;
+      if (nkb > 0) issue_tile(0, tile, with_v);
       __builtin_amdgcn_s_waitcnt(kWaitVm0);
       __syncthreads();
       int it = 0;
       for (; it < active; ++it) {
         const int cur = it & 1;
-        if (it + 1 < nkb) issue_tile(cur ^ 1, seq(it + 1), with_v);
-        body(cur, seq(it));
+        const int nt = next(tile);
+        if (it + 1 < nkb) issue_tile(cur ^ 1, nt, with_v);
+        body(cur, tile);
         __builtin_amdgcn_s_waitcnt(kWaitVm0);
         __syncthreads();
+        tile = nt;
       }
       for (; it < nkb; ++it) {
-        if (it + 1 < nkb) issue_tile((it & 1) ^ 1, seq(it + 1), with_v);
+        const int nt = next(tile);
+        if (it + 1 < nkb) issue_tile((it & 1) ^ 1, nt, with_v);
         __builtin_amdgcn_s_waitcnt(kWaitVm0);
         __syncthreads();
+        tile = nt;
       }
     }
   };
@@ -340,7 +346,7 @@ attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg
     tile_dots(buf, s);
     dots_to_gaps(buf, k0, row_max, raw_max_bf, gap_scaled, s);
   };
-  auto natural = [](int it) { return it; };
+  auto natural = [](int t) { return t + 1; };  // successor in key order
   // Rows of at most two tiles (RES == 2) keep each tile's values in registers
   // across the sweeps: the dot products of sweep A become the gaps and then
   // the weights e of sweep B, and sweep C reuses those e (the same values it
@@ -463,16 +469,8 @@ attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg
     // arrays are indexed statically: the running residue's partials live in
     // acc[], a finished residue is shifted into hist[] (oldest first), and a
     // finished warp's sum is shifted into warp_sum[].
-    auto resmajor = [&](int it) {
-      int r = 0;
-      int acc = 0;
-      while (true) {
-        const int cnt = (nkb - r + 31) / 32;  // tiles with residue r
-        if (it < acc + cnt) return r + 32 * (it - acc);
-        acc += cnt;
-        ++r;
-      }
-    };
+    // successor in residue-major order: tiles r, r + 32, r + 64, ..., then r + 1
+    auto resmajor = [&](int t) { return t + 32 < nkb ? t + 32 : (t & 31) + 1; };
     float warp_sum[8];
     float hist[4][8];  // the current warp's finished residues, in order
     float acc[8];      // [vector slot 4*kb32 + i] of the running residue
