@@ -316,8 +316,7 @@ attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg
     for (int kb32 = 0; kb32 < 2; ++kb32) {
 #pragma unroll
       for (int r = 0; r < 16; r += 2) {
-        const uint32_t pk = pack_bf16x2(s[kb32][r], s[kb32][r + 1]);
-        float v0 = lo_bf16(pk), v1 = hi_bf16(pk);
+        float v0 = round_bf16(s[kb32][r]), v1 = round_bf16(s[kb32][r + 1]);
         if constexpr (POW2_SCALE) {
           v0 = v0 - raw_max_bf;
           v1 = v1 - raw_max_bf;

@@ -36,9 +36,22 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
 }
 
-// Round a float to the nearest bf16 value and return it as float.
+// Round a float to the nearest bf16 value and return it as float: one
+// v_cvt_pk_bf16_f32 with bf16(0) = 0 in the low half and bf16(v) in the high
+// half is exactly the fp32 encoding of bf16(v), so no unpacking follows.  The
+// zero comes through an empty asm (one register per kernel after CSE): with a
+// literal 0 the compiler rewrites the conversion into a convert to the low
+// half plus a shift.  (The conversion itself must stay a compiler-visible
+// instruction: as inline asm it could read an MFMA result before the MFMA
+// has written it, since hazards around asm operands are not tracked.)
+__device__ __forceinline__ float opaque_zero() {
+  float z;
+  asm("v_mov_b32 %0, 0" : "=v"(z));
+  return z;
+}
 __device__ __forceinline__ float round_bf16(float v) {
-  return bf16_to_f32(f32_to_bf16(v));
+  const f32x2 pair = {opaque_zero(), v};
+  return __builtin_bit_cast(float, __builtin_convertvector(pair, bf16x2));
 }
 
 __device__ __forceinline__ float lo_bf16(uint32_t w) { return __uint_as_float(w << 16); }
