@@ -232,3 +232,24 @@ def test_profiling_summary_scales_counters_by_the_copy_calibration(tmp_path):
     assert table["bytes_per_launch"] == 200 * 2048 + 50 * 1024
     text = out.read_text()
     assert "gemm_big_kernel<256, 128>" in text and "spin_kernel" not in text
+
+
+def test_profiling_summary_reports_mfma_utilisation(tmp_path):
+    stats_header = ["Name", "Calls", "TotalDurationNs", "AverageNs", "Percentage", "MinNs", "MaxNs", "StdDev"]
+    gemm = "void enc::(anonymous namespace)::gemm_big_kernel<256, 128>(unsigned short const*)"
+    _write_csv(tmp_path / "trace" / "run_kernel_stats.csv", stats_header, [[gemm, 2, 200.0, 100.0, 100.0, 90, 110, 1.0]])
+    pmc_header = ["Correlation_Id", "Dispatch_Id", "Agent_Id", "Queue_Id", "Process_Id", "Thread_Id", "Grid_Size",
+                  "Kernel_Id", "Kernel_Name", "Workgroup_Size", "LDS_Block_Size", "Scratch_Size", "VGPR_Count",
+                  "Accum_VGPR_Count", "SGPR_Count", "Counter_Name", "Counter_Value", "Start_Timestamp", "End_Timestamp"]
+    rows = []
+    # dispatch 1: busy 1024 SIMDs x 400 cycles of 8 XCDs x 1000 active -> 40%; dispatch 2: 60%
+    for i, busy in ((1, 409600.0), (2, 614400.0)):
+        rows.append([i, i, "Agent 1", 1, 1, 1, 256, 1, gemm, 256, 0, 0, 64, 0, 32, "SQ_VALU_MFMA_BUSY_CYCLES", busy, 0, 1])
+        rows.append([i, i, "Agent 1", 1, 1, 1, 256, 1, gemm, 256, 0, 0, 64, 0, 32, "GRBM_GUI_ACTIVE", 8000.0, 0, 1])
+    _write_csv(tmp_path / "mfma" / "run_counter_collection.csv", pmc_header, rows)
+    util, n = profiling.mfma_utilisation(str(tmp_path / "mfma"), "gemm_big_kernel<256, 128>", 1024, 8)
+    assert n == 2 and util == pytest.approx(0.5)
+    out = tmp_path / "summary.md"
+    assert profiling.main(["--trace", str(tmp_path / "trace"), "--mfma", str(tmp_path / "mfma"), "--workload", "cX",
+                           "--label", "gemm=gemm_big_kernel<256, 128>", "--out", str(out)]) == 0
+    assert "| gemm (`gemm_big_kernel<256, 128>`) | 2 | 50.0% |" in out.read_text()

@@ -13,7 +13,12 @@ The rocprofv3 half reads the CSV files ``rocprofv3 --output-format csv`` writes:
 * ``<run>_kernel_stats.csv`` of a ``--kernel-trace --stats`` run: calls and
   average / total duration per kernel;
 * ``<run>_counter_collection.csv`` of a ``--pmc FETCH_SIZE`` run and of a
-  ``--pmc WRITE_SIZE`` run (one counter set per run): KiB per dispatch.
+  ``--pmc WRITE_SIZE`` run (one counter set per run): KiB per dispatch;
+* optionally the same file of a ``--pmc SQ_VALU_MFMA_BUSY_CYCLES
+  GRBM_GUI_ACTIVE`` run: MFMA utilisation per dispatch, rocprofv3's
+  ``MfmaUtil`` = busy MFMA cycles summed over the SIMDs / (GPU-active cycles of
+  one XCD x SIMD count).  The CSV holds GRBM_GUI_ACTIVE summed over the XCDs,
+  so one XCD's count is that sum over the XCD count.
 
 Counter values are scaled by what the same counter reads for a device copy of
 known size in the same process (``bench.py --copy-calibration-mib N`` ends
@@ -235,6 +240,25 @@ def calibration(values: Dict[str, List[float]], copy_mib: int) -> float:
     return copy_mib * 1024.0 * 1024.0 / max(copies)
 
 
+def mfma_utilisation(directory: str, pattern: str, simds: int, xcds: int) -> Tuple[float, int]:
+    """Mean MfmaUtil (fraction) over the dispatches of the kernels matching
+    pattern, from one run that collected SQ_VALU_MFMA_BUSY_CYCLES and
+    GRBM_GUI_ACTIVE."""
+    busy = read_counter(directory, "SQ_VALU_MFMA_BUSY_CYCLES")
+    active = read_counter(directory, "GRBM_GUI_ACTIVE")
+    names = match(list(busy), pattern)
+    if not names:
+        raise ValueError(f"no profiled kernel matches {pattern!r}")
+    fractions = []
+    for n in names:
+        for b, a in zip(busy[n], active.get(n, [])):
+            if a > 0:
+                fractions.append(b / (a / xcds * simds))
+    if not fractions:
+        raise ValueError(f"no GRBM_GUI_ACTIVE values for {pattern!r}")
+    return sum(fractions) / len(fractions), len(fractions)
+
+
 def match(names: Sequence[str], pattern: str) -> List[str]:
     return [n for n in names if pattern in n]
 
@@ -271,6 +295,9 @@ def main(argv: Optional[Sequence[str]] = None) -> int:
     p.add_argument("--fetch", help="output dir of the --pmc FETCH_SIZE run")
     p.add_argument("--write", help="output dir of the --pmc WRITE_SIZE run")
     p.add_argument("--copy-mib", type=int, default=0, help="size of bench.py's calibration copy")
+    p.add_argument("--mfma", help="output dir of the --pmc SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE run")
+    p.add_argument("--simds", type=int, default=1024, help="SIMDs of the device (MI355X: 256 CUs x 4)")
+    p.add_argument("--xcds", type=int, default=8, help="XCDs of the device (GRBM_GUI_ACTIVE instances)")
     p.add_argument("--workload", required=True)
     p.add_argument("--label", action="append", default=[],
                    help="LABEL=PATTERN: bench kernel label and a substring of its rocprof name")
@@ -337,6 +364,19 @@ def main(argv: Optional[Sequence[str]] = None) -> int:
             with open(args.traffic, "w") as fh:
                 json.dump(table, fh, indent=1, sort_keys=True)
                 fh.write("\n")
+        doc.append("")
+    if args.mfma and args.label:
+        doc.append(
+            "MFMA utilisation per dispatch (PMC run; rocprofv3's MfmaUtil: SQ_VALU_MFMA_BUSY_CYCLES over "
+            f"{args.simds} SIMDs x GRBM_GUI_ACTIVE of one of {args.xcds} XCDs):"
+        )
+        doc.append("")
+        doc.append("| kernel | dispatches | MFMA busy |")
+        doc.append("|---|---:|---:|")
+        for item in args.label:
+            label, pattern = item.split("=", 1)
+            util, n = mfma_utilisation(args.mfma, pattern, args.simds, args.xcds)
+            doc.append(f"| {label} (`{pattern}`) | {n} | {100 * util:.1f}% |")
         doc.append("")
     with open(args.out, "w") as fh:
         fh.write("\n".join(doc))
