@@ -344,9 +344,12 @@ struct BigTile {
   __device__ static constexpr int swz(int row) { return kChunks == 8 ? (row & 7) : ((row >> 1) & 3); }
 };
 
+// r / keep: the residual's 8 values and the row-mask verdict, loaded ahead
+// by the caller (residual epilogues only).
 template <int EPI>
 __device__ __forceinline__ void finish8(const GemmEpilogueArgs& ep, int N, int row, int col,
-                                        const float (&y)[8]) {
+                                        const float (&y)[8], u32x4 r = u32x4{0u, 0u, 0u, 0u},
+                                        bool keep = true) {
   const int64_t idx = static_cast<int64_t>(row) * N + col;
   u32x4 w;
   if constexpr (EPI == kEpiBias) {
@@ -357,9 +360,6 @@ __device__ __forceinline__ void finish8(const GemmEpilogueArgs& ep, int N, int r
     for (int e = 0; e < 8; ++e) g[e] = gelu_erf(y[e]);
     w = u32x4{pack_bf16x2(g[0], g[1]), pack_bf16x2(g[2], g[3]), pack_bf16x2(g[4], g[5]), pack_bf16x2(g[6], g[7])};
   } else {
-    const u32x4 r = *reinterpret_cast<const u32x4*>(ep.residual + idx);
-    bool keep = true;
-    if (ep.row_mask != nullptr) keep = ep.row_mask[row] != 0;
     if (keep) {
       float o[8];
 #pragma unroll
@@ -552,6 +552,30 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
   k_block(kt, stage, 0, false, false);
 
   // ---- epilogue: y = bf16(acc + bias) into LDS, then 8 outputs per thread ----
+  constexpr int kPerRow = BN / 8;
+  constexpr int kRowsPerPass = kThreads / kPerRow;
+  constexpr int kPasses = BM / kRowsPerPass;
+  constexpr bool kResidual = EPI == kEpiResidualKeep || EPI == kEpiResidualZero;
+  const int c8 = (tid % kPerRow) * 8;
+  const int rl0 = tid / kPerRow;
+  // The residual rows (and row-mask bytes) of the first kDepth passes are
+  // requested before the outputs are read back, and pass p requests pass
+  // p + kDepth, so the memory latency overlaps the staging and the passes
+  // instead of costing one round trip per pass.  Rows past M read row M-1 and
+  // are never stored.
+  constexpr int kDepth = kPasses < 2048 / BN ? kPasses : 2048 / BN;  // 16 or 8: within the register budget
+  u32x4 res[kResidual ? kDepth : 1];
+  bool keep[kResidual ? kDepth : 1];
+  auto load_residual = [&](int p, u32x4& r, bool& k) {
+    const int row = min(m0 + rl0 + p * kRowsPerPass, M - 1);
+    r = *reinterpret_cast<const u32x4*>(ep.residual + static_cast<int64_t>(row) * N + n0 + c8);
+    k = ep.row_mask == nullptr || ep.row_mask[row] != 0;
+  };
+  // (256-wide tiles: requested after the staging, which needs the registers)
+  if constexpr (kResidual && BN <= 128) {
+#pragma unroll
+    for (int p = 0; p < kDepth; ++p) load_residual(p, res[p], keep[p]);
+  }
   bf16_t* sc = smem;  // every wave passed the last barrier: the stages are free
 #pragma unroll
   for (int j = 0; j < RN; ++j) {
@@ -566,27 +590,36 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
       }
     }
   }
+  if constexpr (kResidual && BN > 128) {
+#pragma unroll
+    for (int p = 0; p < kDepth; ++p) load_residual(p, res[p], keep[p]);
+  }
   __syncthreads();
 
   if constexpr (EPI != kEpiQkvHeadMajor) {
-    constexpr int kPerRow = BN / 8;
-    constexpr int kRowsPerPass = kThreads / kPerRow;
-    const int c8 = (tid % kPerRow) * 8;
-    for (int rl = tid / kPerRow; rl < BM; rl += kRowsPerPass) {
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p) {
+      const int rl = rl0 + p * kRowsPerPass;
       const int row = m0 + rl;
-      if (row >= M) break;
-      const u32x4 v = *reinterpret_cast<const u32x4*>(sc + rl * T::kLdc + c8);
-      const float y[8] = {lo_bf16(v[0]), hi_bf16(v[0]), lo_bf16(v[1]), hi_bf16(v[1]),
-                          lo_bf16(v[2]), hi_bf16(v[2]), lo_bf16(v[3]), hi_bf16(v[3])};
-      finish8<EPI>(ep, N, row, n0 + c8, y);
+      if (row < M) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(sc + rl * T::kLdc + c8);
+        const float y[8] = {lo_bf16(v[0]), hi_bf16(v[0]), lo_bf16(v[1]), hi_bf16(v[1]),
+                            lo_bf16(v[2]), hi_bf16(v[2]), lo_bf16(v[3]), hi_bf16(v[3])};
+        if constexpr (kResidual) {
+          finish8<EPI>(ep, N, row, n0 + c8, y, res[p % kDepth], keep[p % kDepth]);
+        } else {
+          finish8<EPI>(ep, N, row, n0 + c8, y);
+        }
+      }
+      if constexpr (kResidual) {
+        if (p + kDepth < kPasses) load_residual(p + kDepth, res[p % kDepth], keep[p % kDepth]);
+      }
     }
   } else {
     const int D = ep.d_model;
     const int hd = ep.head_dim;
     const int S = ep.seq_len;
     // Q / K: 8 consecutive channels of one head, one row
-    constexpr int kPerRow = BN / 8;
-    const int c8 = (tid % kPerRow) * 8;
     const int col = n0 + c8;
     const int which = col / D;
     if (which < 2) {
