@@ -54,7 +54,7 @@ const char* enc_last_error(void);
  *   y[r, :] = bf16(gamma * ((x[r, :] - mean) * rsqrt(var + eps)) + beta)
  * If row_mask is non-null, rows with row_mask[r] == 0 are written as zeros
  * (the masked_fill that follows final_norm).  width is a power of two in
- * [256, 4096].  The statistics follow torch's ROCm LayerNorm operation for
+ * [32, 4096].  The statistics follow torch's ROCm LayerNorm operation for
  * operation, so the bf16 output equals nn.LayerNorm's bit for bit.
  * Replaces nn.LayerNorm at transformer_benchmark/models.py:721,723,907 and the
  * case-6 kernel wrapper transformer_benchmark/case6_exact_layer_norm.py:98-121
@@ -103,7 +103,8 @@ int enc_qkv_proj_bf16(const void* x, const void* weight, const void* bias,
  * key_mask[b, j] == 0.  With kv_len, query rows i >= kv_len[b] are padding and
  * are written as zeros.  A query row with no allowed key is written as zeros.
  * context: [batch, seq_len, num_heads * head_dim] (token-major, the layout
- * out_proj consumes).  head_dim == 64; v_t as produced by enc_qkv_proj_bf16.
+ * out_proj consumes).  head_dim is 32, 64 or 128; v_t as produced by
+ * enc_qkv_proj_bf16.
  * Replaces transformer_benchmark/models.py:55-75 (baseline) and the
  * candidate's score/softmax/PV kernels: triangular_scores.py:110-291,
  * pv_context.py:79-542, native_softmax_bf16.py:129-184,
@@ -115,7 +116,8 @@ int enc_attention_fwd_bf16(const void* q, const void* k, const void* v_t,
                            const uint8_t* key_mask, void* stream);
 
 /* One-pass attention with an online softmax: same arguments, masking and
- * layouts as enc_attention_fwd_bf16, any seq_len.  Scores are rounded as the
+ * layouts as enc_attention_fwd_bf16, any seq_len, head_dim 64 only.  Scores
+ * are rounded as the
  * reference rounds them, but the exponentials exp(s_ij - m_i) are rounded to
  * bf16 before the division by the row sum instead of after it, so the context
  * differs from the reference's by bf16 rounding noise of the weights.  That

@@ -12,7 +12,12 @@ import torch
 
 from oracle.encoder_oracle import compare, encoder_forward, encoder_forward_sequences
 from tiktoktechjam2026track3_amd import native
-from tiktoktechjam2026track3_amd.cases import ENCODER_CONFIGS, TransformerConfig, generate_random_case
+from tiktoktechjam2026track3_amd.cases import (
+    ENCODER_CONFIGS,
+    OFFICIAL_TEST_CASES,
+    TransformerConfig,
+    generate_random_case,
+)
 from tiktoktechjam2026track3_amd.models import BaselineTransformer, UserOptimizedTransformer, copy_model_weights
 
 pytestmark = pytest.mark.gpu
@@ -51,6 +56,33 @@ def test_encoder_parity(device, name):
     assert result["passed"], result
     if not bool(mask.all()):
         assert torch.all(out[~mask] == 0)
+
+
+# Official cases the kernels cover: d_model 128 at head dims 32 (1-6, 12, 13),
+# 128 (9) and 64 (10).  Case 14 is c5's shape (the slow test below); cases 7
+# and 11 (head dim 8) and 8 (head dim 256) are rejected as unsupported.
+OFFICIAL_COVERED = (1, 2, 3, 4, 5, 6, 9, 10, 12, 13)
+
+
+@pytest.mark.parametrize("case_id", OFFICIAL_COVERED)
+def test_encoder_parity_official_cases(device, case_id):
+    """Four causal layers at d_model 128 / ffn 128 against the oracle, on the
+    reference runner's default input (seed 1234, no padding) and on a padded
+    variant; the bitwise share is printed for the record."""
+    cfg = OFFICIAL_TEST_CASES[case_id - 1]
+    sd, candidate = build_models(cfg, 1234, device)
+    for padding in (0.0, 0.25):
+        with torch.inference_mode():
+            x, mask = generate_random_case(cfg, device, torch.bfloat16, 1234, padding, 1.0)
+            out = candidate(x, mask)
+            ref = encoder_forward(sd, x, mask, cfg.causal, cfg.num_heads, cfg.num_layers)
+            torch.cuda.synchronize()
+        result = compare(ref, out, RTOL, ATOL)
+        bitwise = float((ref.view(torch.int16) == out.view(torch.int16)).float().mean())
+        print(f"[parity] official case {case_id} padding {padding}: {result} bitwise={bitwise:.6f}", flush=True)
+        assert result["passed"], result
+        if padding > 0:
+            assert torch.all(out[~mask] == 0)
 
 
 def test_encoder_parity_second_trial_c4(device):

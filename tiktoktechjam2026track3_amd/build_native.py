@@ -22,7 +22,16 @@ LIBRARY_NAME = "libmi355x_encoder.so"
 LIBRARY_PATH = PACKAGE_DIR / LIBRARY_NAME
 OFFLOAD_ARCH = "gfx950"
 
-SOURCES = ("layernorm.hip", "gemm.hip", "attention.hip", "flash_attention.hip", "capi.hip")
+SOURCES = (
+    "layernorm.hip",
+    "gemm.hip",
+    "attention.hip",
+    "attention_hd32.hip",
+    "attention_hd64.hip",
+    "attention_hd128.hip",
+    "flash_attention.hip",
+    "capi.hip",
+)
 
 # Packed FP32 VALU ops (v_pk_fma_f32 and friends) are disabled for every device
 # compile; hipcc's host pass prints a harmless "not a recognized feature" note.
@@ -46,7 +55,9 @@ COMMON_FLAGS = (
 # v_accvgpr_read per score.  The GEMM keeps the compiler's choice: its large
 # accumulator tiles live in AGPRs.
 EXTRA_FLAGS = {
-    "attention.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form"),
+    "attention_hd32.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form"),
+    "attention_hd64.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form"),
+    "attention_hd128.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form"),
     "flash_attention.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form"),
 }
 
@@ -111,7 +122,13 @@ def _check_launch_stubs(path: Path) -> None:
     if nm is None:
         return
     proc = subprocess.run([nm, "-D", "--undefined-only", str(path)], capture_output=True, text=True)
-    missing = [line.split()[-1] for line in proc.stdout.splitlines() if "__device_stub__" in line]
+    # A dropped stub shows up either as the stub itself or as the kernel's
+    # host-side handle (the kernel's own mangled name, in namespace enc).
+    missing = [
+        line.split()[-1]
+        for line in proc.stdout.splitlines()
+        if "__device_stub__" in line or "_ZN3enc" in line
+    ]
     if missing:
         raise RuntimeError(f"{path.name}: {len(missing)} kernel launch stub(s) missing, e.g. {missing[0]}")
 

@@ -1,692 +1,13 @@
-// Streaming multi-head attention forward for gfx950, head_dim = 64, bitwise
-// equal to the reference's materialised softmax attention.
-//
-// Scores are never materialised: each workgroup owns BQ = NW * 32 query rows
-// of one (batch, head) (32 per wavefront) and streams 64-key tiles of K (and
-// V^T) through a two-stage LDS ring filled with direct global->LDS loads
-// (global_load_lds_dwordx4).  Both products put the query on the MFMA N
-// dimension (the lane), so every per-query quantity lives in the lane that owns
-// the query (lane l: query l%32, key half l/32):
-//   S^T[key, q]  = K[key, :] . Q[q, :]        A = K tile (LDS), B = Q (registers)
-//   O^T[d, q]   += V^T[d, key] . P^T[key, q]  A = V^T tile (LDS), B = P (registers)
-// The K fragment's MFMA row r is fed key perm(r) = 16(i>>1) + 8h + 4(i&1) + j for
-// r = 8i + 4h + j, which leaves lane half h holding, for each 16-key group kk,
-// keys 16kk + 8h + e (e = 0..7) in consecutive accumulator registers: exactly the
-// B operand of the PV MFMA with the reduction index in natural key order, so PV
-// accumulates keys in the same order as the reference's matmul(P, V).
-//
-// Numerics reproduce transformer_benchmark/models.py:55-70 bit for bit:
-//   s = bf16(bf16(q.k) * scale)                 (MFMA, fp32 accumulate, rounded)
-//   p = bf16(softmax_fp32(s))                   (torch.softmax in fp32, then bf16)
-//   context = bf16(sum_j p_j v_j)               (MFMA, fp32 accumulate)
-// torch's ROCm softmax computes p differently for the two row-length regimes:
-//   rows of <= 2048 keys: e = expf(s - max) (device-library expf), p = e / sum;
-//   longer rows:          e = exp2(rn(s - max) * log2(e)) on the hardware exp
-//                         unit, p = e * (1 / sum) with a correctly rounded 1 / sum.
-// The softmax sum is accumulated in the order torch's ROCm softmax uses:
-//   rows of <= 2048 keys (persistent warp softmax): "lane" lam = key % 64 sums its
-//     keys lam, lam+64, ... in order, then a 64-lane butterfly;
-//   longer rows (block softmax): "thread" t of 512 sums the 4-key vectors t,
-//     t+512, ... in order, then a shuffle-down tree inside each 64-thread warp and
-//     a tree over the 8 warp sums.
-// Both orders were pinned against torch.softmax on an MI355X by fingerprinting
-// the reduction tree.  Because p is rounded after normalisation, the kernel
-// sweeps the keys three times: (A) row max, (B) row sum, (C) probabilities + PV.
-//
-// Cost notes.  The kernel is bound by VALU work per score, not by the MFMAs:
-//   * sweep A takes the max of the raw fp32 dot products and rounds it once at
-//     the end; rounding to bf16 (and scaling by a positive scale) is monotonic,
-//     so max(bf16(x)) = bf16(max(x));
-//   * the division of the short-row regime, p = RN(e / sum), is evaluated as
-//     q0 = RN(e * r), rem = fma(-q0, sum, e), p = fma(rem, r, q0) with
-//     r = RN(1 / sum): Markstein's correction step, which gives the correctly
-//     rounded quotient whenever no intermediate underflows.  Rows whose
-//     smallest weight could underflow (min s - max < -69, e < 2^-100) use the
-//     IEEE division instead (one branch per wavefront).
-// In sweep B for long rows, tiles are visited residue-major (tile n = r + 32m,
-// r = 0..31) so each 512-thread "thread" partial is completed in key order and
-// each warp's 64 partials are live in registers only while that warp is summed.
-//
-// Tile skipping: with causal masking a workgroup stops at the last key tile its
-// last query can see, and a wavefront skips the MFMAs of tiles in its future;
-// with prefix padding (kv_len) key tiles past kv_len are never loaded and query
-// tiles past kv_len are written as zeros.  Skipped keys contribute exp(-inf) = 0
-// in the reference, and adding 0 leaves a partial sum unchanged, so skipping
-// them is exact.
-#include "common.h"
-#include "kernels.h"
+// Exact attention entry (head-dim dispatch), the key-mask length kernel and
+// the expf self-check.  The exact attention kernel itself is a template over
+// the head dim (attention_exact.h), instantiated once per head dim in
+// attention_hd32.hip, attention_hd64.hip and attention_hd128.hip so the three
+// compile in parallel.
+#include "attention_exact.h"
 
 namespace enc {
 
 namespace {
-
-constexpr int kHd = 64;
-constexpr int kBKV = 64;                   // keys per tile
-constexpr int kTileElems = kBKV * kHd;     // one K or V^T tile, bf16 elements
-constexpr int kWarpSoftmaxMaxKeys = 2048;  // rows up to this length use the warp order
-constexpr float kLog2e = 1.44269504088896340736f;
-// below this weight (s - max < -69.3) the Markstein quotient is not used
-constexpr float kMinFastGap = -69.0f;
-
-enum MaskMode : int { kMaskNone = 0, kMaskPrefix = 1, kMaskBytes = 2 };
-
-// LDS tile = 64 rows (keys of K, head channels of V^T) x 8 chunks of 16 bytes.
-// Chunk c of row r sits in slot c ^ (r & 7), so the 32 rows one MFMA fragment
-// read touches at a fixed chunk fall in distinct bank groups.
-__device__ __forceinline__ int tile_off(int row, int chunk) { return row * kHd + ((chunk ^ (row & 7)) << 3); }
-
-// s_waitcnt immediate: wait until no vector-memory operation is outstanding
-// (expcnt and lgkmcnt left at their no-wait maxima; gfx9 encoding).
-constexpr int kWaitVm0 = (7 << 4) | (15 << 8);
-
-// key offset inside a 64-key tile held by accumulator register r of block kb32
-// in lane half h (see the permutation above)
-__device__ __forceinline__ int tile_key(int kb32, int r, int h) {
-  const int i = r >> 2, j = r & 3;
-  return 32 * kb32 + 16 * (i >> 1) + 8 * h + 4 * (i & 1) + j;
-}
-
-// RES > 0: short rows (at most RES tiles): every K/V tile is loaded into LDS
-// once and the three sweeps read them from there, with no further loads or
-// barriers.  RES == 0: the two-stage ring streams the tiles for each sweep.
-template <int NW, bool CAUSAL, int MASK, bool POW2_SCALE, bool BLOCK_ORDER, int RES>
-__global__ void __launch_bounds__(NW * kWave)
-attn_fwd_hd64_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
-                     const bf16_t* __restrict__ Vt, bf16_t* __restrict__ ctx, int H, int S,
-                     int ld_vt, int num_qblocks, float scale,
-                     const int32_t* __restrict__ kv_len, const uint8_t* __restrict__ key_mask) {
-  constexpr int kThreads = NW * kWave;
-  constexpr int kBQ = NW * 32;
-  // K, V^T and key-mask tiles live in dynamic LDS sized at launch
-  // (attn_lds_bytes): a static __shared__ array whose size depends on a
-  // template parameter loses the kernel's host launch stub in this compiler.
-  constexpr int kBufs = RES > 0 ? RES : 2;
-  extern __shared__ __attribute__((aligned(16))) bf16_t attn_lds[];
-  bf16_t (*sK)[kTileElems] = reinterpret_cast<bf16_t (*)[kTileElems]>(attn_lds);
-  bf16_t (*sV)[kTileElems] = reinterpret_cast<bf16_t (*)[kTileElems]>(attn_lds + kBufs * kTileElems);
-  uint8_t (*sM)[kBKV] = reinterpret_cast<uint8_t (*)[kBKV]>(attn_lds + 2 * kBufs * kTileElems);
-
-  // Block -> (batch*head, query tile).  Non-causal: MI355X hands consecutive
-  // workgroups to its 8 XCDs round-robin; the id is remapped so each XCD walks
-  // a contiguous run of query tiles of one head, whose K/V then stream through
-  // that XCD's L2 once for all of them.  Causal: heads vary fastest and query
-  // tiles run last-to-first, so the heaviest tiles (most keys) start first.
-  const int nblocks = static_cast<int>(gridDim.x);
-  const int num_bh = nblocks / num_qblocks;
-  int bh, qb;
-  if constexpr (CAUSAL) {
-    const int id = blockIdx.x;
-    bh = id % num_bh;
-    qb = num_qblocks - 1 - id / num_bh;
-  } else {
-    const int pid = blockIdx.x;
-    const int xcd = pid % 8, slot = pid / 8;
-    const int base = nblocks / 8, rem = nblocks % 8;
-    const int id = xcd * base + min(xcd, rem) + slot;
-    qb = id % num_qblocks;
-    bh = id / num_qblocks;
-  }
-  const int b = bh / H;
-  const int h = bh - b * H;
-  const int q0 = qb * kBQ;
-  const int D = H * kHd;
-
-  const int tid = threadIdx.x;
-  const int lane = tid % kWave;
-  // wavefront index as a scalar, so per-tile decisions stay uniform branches
-  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
-  const int l32 = lane & 31;
-  const int lhi = lane >> 5;
-  const int qrow = q0 + wave * 32 + l32;  // the query this lane owns
-
-  int kv_limit = S;  // keys >= kv_limit are excluded
-  if constexpr (MASK == kMaskPrefix) kv_limit = min(S, static_cast<int>(kv_len[b]));
-
-  bf16_t* ctx_row = ctx + (static_cast<int64_t>(b) * S + qrow) * D + h * kHd;
-
-  if (MASK == kMaskPrefix && q0 >= kv_limit) {
-    // Whole query tile is padding: zeros, no work.
-    if (qrow < S) {
-#pragma unroll
-      for (int c = 0; c < 4; ++c)
-        *reinterpret_cast<u32x4*>(ctx_row + lhi * 32 + c * 8) = u32x4{0, 0, 0, 0};
-    }
-    return;
-  }
-
-  int kv_end = kv_limit;
-  if constexpr (CAUSAL) kv_end = min(kv_end, q0 + kBQ);
-  const int nkb = (kv_end + kBKV - 1) / kBKV;
-
-  const int64_t head_off = static_cast<int64_t>(bh) * S * kHd;
-  const bf16_t* Qh = Q + head_off;
-  const bf16_t* Kh = Kg + head_off;
-  const bf16_t* Vh = Vt + static_cast<int64_t>(bh) * kHd * ld_vt;
-  const uint8_t* Mh = (MASK == kMaskBytes) ? key_mask + static_cast<int64_t>(b) * S : nullptr;
-
-  // Q fragments (B operand of S^T): lane (q = l32, k-group lhi) holds
-  // d = 16*ks + 8*lhi .. +8.
-  bf16x8 qf[4];
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    if (qrow < S) {
-      qf[ks] = *reinterpret_cast<const bf16x8*>(Qh + static_cast<int64_t>(qrow) * kHd + ks * 16 + lhi * 8);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) qf[ks][e] = static_cast<__bf16>(0.f);
-    }
-  }
-  // MFMA row l32 of a 32-key block reads K row perm(l32)
-  const int krow = 16 * ((l32 >> 3) >> 1) + 8 * ((l32 >> 2) & 1) + 4 * ((l32 >> 3) & 1) + (l32 & 3);
-
-  // ---- tile loads ----
-  // Full tiles: load instruction j of wavefront w fills LDS rows 8(NW j + w) ..
-  // +7 (64 lanes x 16 bytes, consecutive); lane L writes row 8(NW j + w) + L/8,
-  // slot L%8, which holds chunk (L%8) ^ (L/8) of that row.
-  const int ld_row = lane >> 3;
-  const int ld_chunk = (lane & 7) ^ ld_row;
-  auto issue_full = [&](int buf, int k0, bool with_v) {
-#pragma unroll
-    for (int j = 0; j < 8 / NW; ++j) {
-      const int row0 = 8 * (NW * j + wave);
-      const int row = row0 + ld_row;
-      __builtin_amdgcn_global_load_lds(Kh + static_cast<int64_t>(k0 + row) * kHd + ld_chunk * 8,
-                                       &sK[buf][row0 * kHd], 16, 0, 0);
-      if (with_v)
-        __builtin_amdgcn_global_load_lds(Vh + static_cast<int64_t>(row) * ld_vt + k0 + ld_chunk * 8,
-                                         &sV[buf][row0 * kHd], 16, 0, 0);
-    }
-  };
-  // The tile that crosses seq_len goes through registers: keys >= S read as
-  // zeros (V^T's padding columns are never read, so they may hold anything).
-  auto load_edge = [&](int buf, int k0, bool with_v) {
-    for (int c = tid; c < kBKV * 8; c += kThreads) {
-      const int row = c >> 3, chunk = c & 7;
-      u32x4 kv = u32x4{0, 0, 0, 0};
-      if (k0 + row < S) kv = *reinterpret_cast<const u32x4*>(Kh + static_cast<int64_t>(k0 + row) * kHd + chunk * 8);
-      *reinterpret_cast<u32x4*>(&sK[buf][tile_off(row, chunk)]) = kv;
-      if (!with_v) continue;
-      const int key = k0 + chunk * 8;
-      const bf16_t* vp = Vh + static_cast<int64_t>(row) * ld_vt + key;
-      uint16_t t[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) t[e] = (key + e < S) ? vp[e] : uint16_t(0);
-      *reinterpret_cast<u32x4*>(&sV[buf][tile_off(row, chunk)]) =
-          u32x4{t[0] | (uint32_t(t[1]) << 16), t[2] | (uint32_t(t[3]) << 16),
-                t[4] | (uint32_t(t[5]) << 16), t[6] | (uint32_t(t[7]) << 16)};
-    }
-  };
-  auto issue_tile = [&](int buf, int kb, bool with_v) {
-    const int k0 = kb * kBKV;
-    if (k0 + kBKV <= S) {
-      issue_full(buf, k0, with_v);
-    } else {
-      load_edge(buf, k0, with_v);
-    }
-    if constexpr (MASK == kMaskBytes) {
-      if (tid < kBKV) sM[buf][tid] = (k0 + tid < S) ? Mh[k0 + tid] : uint8_t(0);
-    }
-  };
-
-  // Runs body(buf, tile) over the first `active` of the nkb tiles in the
-  // order 0, next(0), next(next(0)), ..., double-buffered: the loads of the
-  // next tile overlap the current body.  The remaining tiles (a causal
-  // wavefront's future) only take part in the loads and barriers the other
-  // wavefronts need; keeping them out of the body's loop (rather than skipping
-  // the body per tile) keeps the accumulators free of per-tile register
-  // copies.  With resident tiles the body reads tile t from buffer t.
-  bool resident = false;
-  auto sweep = [&](auto next, bool with_v, int active, auto body) {
-    if (RES > 0) {
-      if (!resident) {
-        for (int t = 0; t < nkb; ++t) issue_tile(t, t, true);
-        __builtin_amdgcn_s_waitcnt(kWaitVm0);
-        __syncthreads();
-        resident = true;
-      }
-      int tile = 0;
-      for (int it = 0; it < active; ++it, tile = next(tile)) body(tile, tile);
-    } else {
-      int tile = 0;
-      if (nkb > 0) issue_tile(0, tile, with_v);
-      __builtin_amdgcn_s_waitcnt(kWaitVm0);
-      __syncthreads();
-      int it = 0;
-      for (; it < active; ++it) {
-        const int cur = it & 1;
-        const int nt = next(tile);
-        if (it + 1 < nkb) issue_tile(cur ^ 1, nt, with_v);
-        body(cur, tile);
-        __builtin_amdgcn_s_waitcnt(kWaitVm0);
-        __syncthreads();
-        tile = nt;
-      }
-      for (; it < nkb; ++it) {
-        const int nt = next(tile);
-        if (it + 1 < nkb) issue_tile((it & 1) ^ 1, nt, with_v);
-        __builtin_amdgcn_s_waitcnt(kWaitVm0);
-        __syncthreads();
-        tile = nt;
-      }
-    }
-  };
-
-  const int wq_first = q0 + wave * 32;
-  const int wq_last = wq_first + 31;
-  // tiles of the natural order this wavefront multiplies (causal: those with
-  // a key <= its last query)
-  const int active = CAUSAL ? min(nkb, wq_last / kBKV + 1) : nkb;
-
-  // Raw fp32 dot products of the 64-key tile in LDS buffer `buf`.
-  auto tile_dots = [&](int buf, f32x16 (&s)[2]) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      s[0][r] = 0.f;
-      s[1][r] = 0.f;
-    }
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-#pragma unroll
-      for (int kb32 = 0; kb32 < 2; ++kb32) {
-        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&sK[buf][tile_off(kb32 * 32 + krow, 2 * ks + lhi)]);
-        s[kb32] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], s[kb32], 0, 0, 0);
-      }
-    }
-  };
-  // Whether key (tile offset kl) is allowed for this lane's query.
-  auto key_ok = [&](int buf, int k0, int kl) {
-    const int key = k0 + kl;
-    bool ok = key < kv_limit;
-    if constexpr (CAUSAL) ok = ok && key <= qrow;
-    if constexpr (MASK == kMaskBytes) ok = ok && sM[buf][kl] != 0;
-    return ok;
-  };
-  auto tile_needs_mask = [&](int k0) {
-    return (CAUSAL && k0 + kBKV - 1 > wq_first) || (k0 + kBKV > kv_limit) || (MASK == kMaskBytes);
-  };
-  // Score tile into s[2] as the softmax's first operation sees it:
-  //   g = rn(s - max), s = bf16(bf16(q.k) * scale), excluded keys -inf.
-  // With a power-of-two scale, s = bf16(q.k) * scale exactly and
-  // rn(s - max) = scale * rn(bf16(q.k) - bf16(max raw dot)), so the scale
-  // multiplies the difference (or folds into the exp2 multiplier below).
-  // gap_scaled selects whether the returned g carries the scale.
-  auto dots_to_gaps = [&](int buf, int k0, float row_max, float raw_max_bf, bool gap_scaled,
-                          f32x16 (&s)[2]) {
-#pragma unroll
-    for (int kb32 = 0; kb32 < 2; ++kb32) {
-#pragma unroll
-      for (int r = 0; r < 16; r += 2) {
-        float v0 = round_bf16(s[kb32][r]), v1 = round_bf16(s[kb32][r + 1]);
-        if constexpr (POW2_SCALE) {
-          v0 = v0 - raw_max_bf;
-          v1 = v1 - raw_max_bf;
-          if (gap_scaled) {
-            v0 *= scale;
-            v1 *= scale;
-          }
-        } else {
-          v0 = round_bf16(v0 * scale) - row_max;
-          v1 = round_bf16(v1 * scale) - row_max;
-        }
-        s[kb32][r] = v0;
-        s[kb32][r + 1] = v1;
-      }
-    }
-    if (tile_needs_mask(k0)) {
-#pragma unroll
-      for (int kb32 = 0; kb32 < 2; ++kb32)
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          s[kb32][r] = key_ok(buf, k0, tile_key(kb32, r, lhi)) ? s[kb32][r] : -INFINITY;
-    }
-  };
-  auto tile_gaps = [&](int buf, int k0, float row_max, float raw_max_bf, bool gap_scaled,
-                       f32x16 (&s)[2]) {
-    tile_dots(buf, s);
-    dots_to_gaps(buf, k0, row_max, raw_max_bf, gap_scaled, s);
-  };
-  auto natural = [](int t) { return t + 1; };  // successor in key order
-  // Rows of at most two tiles (RES == 2) keep each tile's values in registers
-  // across the sweeps: the dot products of sweep A become the gaps and then
-  // the weights e of sweep B, and sweep C reuses those e (the same values it
-  // would recompute), so every score's exponential is evaluated once.
-  constexpr bool kCache = RES == 2;
-  f32x16 cache[kCache ? 2 : 1][2];
-  auto load_resident = [&]() {
-    for (int t = 0; t < nkb; ++t) issue_tile(t, t, true);
-    __builtin_amdgcn_s_waitcnt(kWaitVm0);
-    __syncthreads();
-  };
-
-  // ============================ sweep A: row max ============================
-  // max (and, for the short-row regime, min) of the raw dot products of the
-  // allowed keys; the bf16 score of the max is formed once afterwards.
-  float mx = -INFINITY, mn = INFINITY;
-  auto max_body = [&](int buf, int kb, f32x16 (&s)[2]) {
-    const int k0 = kb * kBKV;
-    tile_dots(buf, s);
-    if (tile_needs_mask(k0)) {
-#pragma unroll
-      for (int kb32 = 0; kb32 < 2; ++kb32) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const bool ok = key_ok(buf, k0, tile_key(kb32, r, lhi));
-          mx = fmaxf(mx, ok ? s[kb32][r] : -INFINITY);
-          if constexpr (!BLOCK_ORDER) mn = fminf(mn, ok ? s[kb32][r] : INFINITY);
-        }
-      }
-    } else {
-#pragma unroll
-      for (int r = 0; r < 16; r += 2) {
-        mx = fmaxf(mx, fmaxf(fmaxf(s[0][r], s[0][r + 1]), fmaxf(s[1][r], s[1][r + 1])));
-        if constexpr (!BLOCK_ORDER) mn = fminf(mn, fminf(fminf(s[0][r], s[0][r + 1]), fminf(s[1][r], s[1][r + 1])));
-      }
-    }
-  };
-  if constexpr (kCache) {
-    load_resident();
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-      if (t < active) max_body(t, t, cache[t]);
-  } else {
-    sweep(natural, false, active, [&](int buf, int kb) {
-      f32x16 s[2];
-      max_body(buf, kb, s);
-    });
-  }
-  mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-  auto to_score = [&](float raw) {
-    const float rq = round_bf16(raw);
-    return POW2_SCALE ? rq * scale : round_bf16(rq * scale);
-  };
-  const float row_max = (mx == -INFINITY) ? -INFINITY : to_score(mx);
-  const float raw_max_bf = (mx == -INFINITY) ? -INFINITY : round_bf16(mx);
-  // exp2 multiplier of the long-row regime: log2(e), times the scale when the
-  // gap is kept unscaled (exact: the scale is a power of two)
-  const float c_exp = POW2_SCALE ? scale * kLog2e : kLog2e;
-  bool slow_div = false;
-  if constexpr (!BLOCK_ORDER) {
-    mn = fminf(mn, __shfl_xor(mn, 32, kWave));
-    // weights below 2^-100 could underflow inside the Markstein quotient
-    const bool tiny = (mn != INFINITY) && (to_score(mn) - row_max < kMinFastGap);
-    slow_div = __builtin_amdgcn_ballot_w64(tiny) != 0;
-  }
-
-  // ======================= sweep B: row sum of exp(s - max) =======================
-  float row_sum;
-  if constexpr (!BLOCK_ORDER) {
-    // warp order: partial[lam] over keys lam, lam+64, ... (lam = key % 64)
-    float part[2][16];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      part[0][r] = 0.f;
-      part[1][r] = 0.f;
-    }
-    if constexpr (kCache) {
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        if (t >= active) continue;
-        dots_to_gaps(t, t * kBKV, row_max, raw_max_bf, true, cache[t]);
-#pragma unroll
-        for (int kb32 = 0; kb32 < 2; ++kb32)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            cache[t][kb32][r] = expf_nonpos(cache[t][kb32][r]);
-            part[kb32][r] += cache[t][kb32][r];
-          }
-      }
-    } else {
-      sweep(natural, false, active, [&](int buf, int kb) {
-        const int k0 = kb * kBKV;
-        f32x16 s[2];
-        tile_gaps(buf, k0, row_max, raw_max_bf, true, s);
-#pragma unroll
-        for (int kb32 = 0; kb32 < 2; ++kb32)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) part[kb32][r] += expf_nonpos(s[kb32][r]);
-      });
-    }
-    // 64-lane butterfly; lam bits: 5 = kb32, 4 = i>>1 (reg bit 3), 3 = lane half,
-    // 2 = i&1 (reg bit 2), 1..0 = j (reg bits 1..0)
-    float a[16];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) a[r] = part[0][r] + part[1][r];             // offset 32
-    float c[8];
-#pragma unroll
-    for (int r = 0; r < 8; ++r) c[r] = a[r] + a[r + 8];                      // offset 16
-#pragma unroll
-    for (int r = 0; r < 8; ++r) c[r] = c[r] + __shfl_xor(c[r], 32, kWave);  // offset 8
-    float d4[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) d4[r] = c[r] + c[r + 4];                     // offset 4
-    const float e2a = d4[0] + d4[2], e2b = d4[1] + d4[3];                    // offset 2
-    row_sum = e2a + e2b;                                                     // offset 1
-  } else {
-    // block order: "thread" t (of 512) sums 4-key vectors t, t+512, ...; tile
-    // n = r + 32 m holds the vectors of threads 16 r .. 16 r + 15.  Tiles are
-    // visited residue-major; "warp" w covers residues 4w .. 4w+3.  All partial
-    // arrays are indexed statically: the running residue's partials live in
-    // acc[], a finished residue is shifted into hist[] (oldest first), and a
-    // finished warp's sum is shifted into warp_sum[].
-    // successor in residue-major order: tiles r, r + 32, r + 64, ..., then r + 1
-    auto resmajor = [&](int t) { return t + 32 < nkb ? t + 32 : (t & 31) + 1; };
-    float warp_sum[8];
-    float hist[4][8];  // the current warp's finished residues, in order
-    float acc[8];      // [vector slot 4*kb32 + i] of the running residue
-#pragma unroll
-    for (int w = 0; w < 8; ++w) warp_sum[w] = 0.f;
-#pragma unroll
-    for (int v = 0; v < 8; ++v) {
-      acc[v] = 0.f;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) hist[q][v] = 0.f;
-    }
-    int cur_res = 0;
-    // residue cur_res is complete: shift it into hist; after a warp's fourth
-    // residue, reduce the warp with a shuffle-down tree over
-    // lam = 16 rr + u, u = 8 kb32 + 4 (i>>1) + 2 h + (i&1):
-    // offsets 32, 16 (rr), 8 (kb32), 4 (i>>1), 2 (lane half), 1 (i&1)
-    auto finish_residue = [&]() {
-#pragma unroll
-      for (int v = 0; v < 8; ++v) {
-        hist[0][v] = hist[1][v];
-        hist[1][v] = hist[2][v];
-        hist[2][v] = hist[3][v];
-        hist[3][v] = acc[v];
-        acc[v] = 0.f;
-      }
-      ++cur_res;
-      if ((cur_res & 3) == 0) {
-        float t8[8];
-#pragma unroll
-        for (int v = 0; v < 8; ++v) t8[v] = (hist[0][v] + hist[2][v]) + (hist[1][v] + hist[3][v]);
-        float t4[4];
-#pragma unroll
-        for (int v = 0; v < 4; ++v) t4[v] = t8[v] + t8[v + 4];                   // offset 8 (kb32)
-        float t2[2];
-#pragma unroll
-        for (int v = 0; v < 2; ++v) t2[v] = t4[v] + t4[v + 2];                   // offset 4 (i>>1)
-#pragma unroll
-        for (int v = 0; v < 2; ++v) t2[v] = t2[v] + __shfl_xor(t2[v], 32, kWave);  // offset 2
-        const float ws = t2[0] + t2[1];                                          // offset 1 (i&1)
-#pragma unroll
-        for (int w = 0; w < 7; ++w) warp_sum[w] = warp_sum[w + 1];
-        warp_sum[7] = ws;
-      }
-    };
-    sweep(resmajor, false, nkb, [&](int buf, int kb) {
-      const int k0 = kb * kBKV;
-      const int r = kb & 31;
-      while (cur_res < r) finish_residue();  // uniform
-      if (CAUSAL && k0 > wq_last) return;
-      f32x16 s[2];
-      tile_gaps(buf, k0, row_max, raw_max_bf, false, s);
-#pragma unroll
-      for (int kb32 = 0; kb32 < 2; ++kb32) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float a = acc[4 * kb32 + i];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) a += __builtin_amdgcn_exp2f(s[kb32][4 * i + j] * c_exp);
-          acc[4 * kb32 + i] = a;
-        }
-      }
-    });
-    while (cur_res < 32) finish_residue();
-    // tree over the 8 warp sums (offsets 4, 2, 1)
-    const float a0 = warp_sum[0] + warp_sum[4], a1 = warp_sum[1] + warp_sum[5];
-    const float a2 = warp_sum[2] + warp_sum[6], a3 = warp_sum[3] + warp_sum[7];
-    row_sum = (a0 + a2) + (a1 + a3);
-  }
-
-  // ================== sweep C: p = bf16(softmax), context += P V ==================
-  // Correctly rounded 1 / sum: the block-order epilogue multiplies by it; the
-  // short-row regime uses it as the Markstein reciprocal.
-  const float inv_sum = 1.0f / row_sum;
-  f32x16 o[2];
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    o[0][r] = 0.f;
-    o[1][r] = 0.f;
-  }
-  // s holds the gaps, or (have_e) the weights e themselves
-  auto pv_body = [&](int buf, f32x16 (&s)[2], bool have_e) {
-    bf16x8 pf[4];
-    if (BLOCK_ORDER || !slow_div) {
-#pragma unroll
-      for (int kb32 = 0; kb32 < 2; ++kb32) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float e = have_e ? s[kb32][r]
-                          : BLOCK_ORDER ? __builtin_amdgcn_exp2f(s[kb32][r] * c_exp) : expf_nonpos(s[kb32][r]);
-          float p;
-          if constexpr (BLOCK_ORDER) {
-            p = e * inv_sum;
-          } else {
-            const float q = e * inv_sum;
-            p = fmaf(fmaf(-q, row_sum, e), inv_sum, q);
-          }
-          pf[kb32 * 2 + (r >> 3)][r & 7] = static_cast<__bf16>(p);
-        }
-      }
-    } else {
-#pragma unroll
-      for (int kb32 = 0; kb32 < 2; ++kb32) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float e = have_e ? s[kb32][r] : expf_nonpos(s[kb32][r]);
-          pf[kb32 * 2 + (r >> 3)][r & 7] = static_cast<__bf16>(e / row_sum);
-        }
-      }
-    }
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-#pragma unroll
-      for (int db = 0; db < 2; ++db) {
-        const bf16x8 vf = *reinterpret_cast<const bf16x8*>(&sV[buf][tile_off(db * 32 + l32, 2 * kk + lhi)]);
-        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[kk], o[db], 0, 0, 0);
-      }
-    }
-  };
-  if constexpr (kCache) {
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-      if (t < active) pv_body(t, cache[t], true);
-  } else {
-    sweep(natural, true, active, [&](int buf, int kb) {
-      f32x16 s[2];
-      tile_gaps(buf, kb * kBKV, row_max, raw_max_bf, !BLOCK_ORDER, s);
-      pv_body(buf, s, false);
-    });
-  }
-
-  // ---- write context[b, qrow, h*64 + d] = bf16(O) ----
-  if (qrow < S) {
-    bool zero = !(row_sum > 0.f);
-    if constexpr (MASK == kMaskPrefix) zero = zero || qrow >= kv_limit;
-#pragma unroll
-    for (int db = 0; db < 2; ++db) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int d = db * 32 + 8 * i + 4 * lhi;
-        u32x2 w = {0u, 0u};
-        if (!zero) {
-          w = u32x2{pack_bf16x2(o[db][4 * i], o[db][4 * i + 1]),
-                    pack_bf16x2(o[db][4 * i + 2], o[db][4 * i + 3])};
-        }
-        *reinterpret_cast<u32x2*>(ctx_row + d) = w;
-      }
-    }
-  }
-}
-
-// LDS bytes of one attention workgroup: K and V^T tiles plus key-mask bytes
-constexpr size_t attn_lds_bytes(int res) {
-  return static_cast<size_t>(res > 0 ? res : 2) * (2 * kTileElems * sizeof(bf16_t) + kBKV);
-}
-
-template <int NW, bool CAUSAL, int MASK, bool POW2, bool BLOCK_ORDER, int RES = 0>
-hipError_t launch_attn(const bf16_t* q, const bf16_t* k, const bf16_t* vt, bf16_t* ctx, int B,
-                       int H, int S, float scale, const int32_t* kv_len, const uint8_t* key_mask,
-                       hipStream_t st) {
-  constexpr int kBQ = NW * 32;
-  constexpr size_t kLds = attn_lds_bytes(RES);
-  const int nqb = (S + kBQ - 1) / kBQ;
-  const dim3 grid(static_cast<uint32_t>(B) * H * nqb);
-  const int ld_vt = static_cast<int>(vt_stride(S));
-  auto kernel = attn_fwd_hd64_kernel<NW, CAUSAL, MASK, POW2, BLOCK_ORDER, RES>;
-  if constexpr (kLds > 64 * 1024) {
-    // above 64 KiB of dynamic LDS the kernel has to opt in (once per process)
-    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                       static_cast<int>(kLds));
-    if (attr != hipSuccess) return attr;
-  }
-  hipLaunchKernelGGL(kernel, grid, dim3(NW * kWave), kLds, st, q, k, vt, ctx, H, S, ld_vt, nqb, scale, kv_len,
-                     key_mask);
-  return hipGetLastError();
-}
-
-template <bool CAUSAL, int MASK, bool POW2>
-hipError_t dispatch_order(const bf16_t* q, const bf16_t* k, const bf16_t* vt, bf16_t* ctx, int B,
-                          int H, int S, float scale, const int32_t* kv_len,
-                          const uint8_t* key_mask, hipStream_t st) {
-  if (S > kWarpSoftmaxMaxKeys)
-    return launch_attn<4, CAUSAL, MASK, POW2, true>(q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
-  // Small problems use one-wavefront workgroups (32 queries) so more of the
-  // 256 CUs get work; larger ones share each K/V tile among 4 wavefronts.
-  // Rows of at most 256 keys keep every tile resident in LDS.
-  const int64_t groups128 = static_cast<int64_t>(B) * H * ((S + 127) / 128);
-  if (groups128 < 512) {
-    if (S <= 2 * kBKV)
-      return launch_attn<1, CAUSAL, MASK, POW2, false, 2>(q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
-    if (S <= 4 * kBKV)
-      return launch_attn<1, CAUSAL, MASK, POW2, false, 4>(q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
-    return launch_attn<1, CAUSAL, MASK, POW2, false>(q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
-  }
-  if (S <= 2 * kBKV)
-    return launch_attn<4, CAUSAL, MASK, POW2, false, 2>(q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
-  if (S <= 4 * kBKV)
-    return launch_attn<4, CAUSAL, MASK, POW2, false, 4>(q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
-  return launch_attn<4, CAUSAL, MASK, POW2, false>(q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
-}
-
-template <bool CAUSAL, int MASK>
-hipError_t dispatch_pow2(bool pow2, const bf16_t* q, const bf16_t* k, const bf16_t* vt,
-                         bf16_t* ctx, int B, int H, int S, float scale, const int32_t* kv_len,
-                         const uint8_t* key_mask, hipStream_t st) {
-  if (pow2) return dispatch_order<CAUSAL, MASK, true>(q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
-  return dispatch_order<CAUSAL, MASK, false>(q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
-}
-
-template <bool CAUSAL>
-hipError_t dispatch_mask(int mask, bool pow2, const bf16_t* q, const bf16_t* k, const bf16_t* vt,
-                         bf16_t* ctx, int B, int H, int S, float scale, const int32_t* kv_len,
-                         const uint8_t* key_mask, hipStream_t st) {
-  if (mask == kMaskPrefix) return dispatch_pow2<CAUSAL, kMaskPrefix>(pow2, q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
-  if (mask == kMaskBytes) return dispatch_pow2<CAUSAL, kMaskBytes>(pow2, q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
-  return dispatch_pow2<CAUSAL, kMaskNone>(pow2, q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
-}
 
 __global__ void __launch_bounds__(256)
 mask_lengths_kernel(const uint8_t* __restrict__ mask, int64_t S, int32_t* __restrict__ kv_len) {
@@ -738,15 +59,17 @@ hipError_t attention_fwd_bf16(const bf16_t* q, const bf16_t* k, const bf16_t* v_
                               int batch, int heads, int seq_len, int head_dim, float scale,
                               bool causal, const int32_t* kv_len, const uint8_t* key_mask,
                               hipStream_t stream) {
-  if (head_dim != kHd) return hipErrorInvalidValue;
   if (batch == 0 || seq_len == 0) return hipSuccess;
-  int mant_exp = 0;
-  const float mant = frexpf(scale, &mant_exp);
-  const bool pow2 = (mant == 0.5f);
-  const int mask = key_mask != nullptr ? kMaskBytes : (kv_len != nullptr ? kMaskPrefix : kMaskNone);
-  if (causal)
-    return dispatch_mask<true>(mask, pow2, q, k, v_t, ctx, batch, heads, seq_len, scale, kv_len, key_mask, stream);
-  return dispatch_mask<false>(mask, pow2, q, k, v_t, ctx, batch, heads, seq_len, scale, kv_len, key_mask, stream);
+  switch (head_dim) {
+    case 32:
+      return attention_exact_hd32(q, k, v_t, ctx, batch, heads, seq_len, scale, kv_len, key_mask, causal, stream);
+    case 64:
+      return attention_exact_hd64(q, k, v_t, ctx, batch, heads, seq_len, scale, kv_len, key_mask, causal, stream);
+    case 128:
+      return attention_exact_hd128(q, k, v_t, ctx, batch, heads, seq_len, scale, kv_len, key_mask, causal, stream);
+    default:
+      return hipErrorInvalidValue;
+  }
 }
 
 hipError_t mask_lengths(const uint8_t* mask, int64_t batch, int64_t seq_len, int32_t* kv_len,

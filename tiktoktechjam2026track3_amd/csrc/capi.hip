@@ -85,11 +85,14 @@ int check_encoder_shape(int64_t B, int64_t S, int64_t D, int64_t H, int64_t F, b
   if (!shape_ok(B) || !shape_ok(S) || !shape_ok(D) || !shape_ok(H) || !shape_ok(F))
     return fail(ENC_ERR_INVALID, "batch, seq_len, d_model, num_heads and ffn_dim must be positive");
   if (D % H != 0) return fail(ENC_ERR_INVALID, "d_model must be divisible by num_heads");
-  if (D / H != 64)
-    return fail(ENC_ERR_UNSUPPORTED, "attention kernel supports head_dim == 64 only (got " +
-                                         std::to_string(D / H) + ")");
+  const int64_t hd = D / H;
+  if (exact_attention ? !(hd == 32 || hd == 64 || hd == 128) : hd != 64)
+    return fail(ENC_ERR_UNSUPPORTED,
+                std::string(exact_attention ? "attention kernel supports head_dim 32, 64 or 128"
+                                            : "online attention kernel supports head_dim 64 only") +
+                    " (got " + std::to_string(hd) + ")");
   if (!enc::layernorm_supported(D))
-    return fail(ENC_ERR_UNSUPPORTED, "LayerNorm width must be a power of two in [256, 4096] (got " +
+    return fail(ENC_ERR_UNSUPPORTED, "LayerNorm width must be a power of two in [32, 4096] (got " +
                                          std::to_string(D) + ")");
   if (exact_attention && !enc::attention_seq_supported(S))
     return fail(ENC_ERR_UNSUPPORTED, "seq_len above 2048 must be a multiple of 4 (got " +
@@ -114,7 +117,7 @@ int enc_layernorm_bf16(const void* x, const void* gamma, const void* beta, void*
   if (rows == 0) return ok();
   if (!x || !gamma || !beta || !y) return fail(ENC_ERR_INVALID, "layernorm: null tensor pointer");
   if (!enc::layernorm_supported(width))
-    return fail(ENC_ERR_UNSUPPORTED, "layernorm: width must be a power of two in [256, 4096]");
+    return fail(ENC_ERR_UNSUPPORTED, "layernorm: width must be a power of two in [32, 4096]");
   if (!(eps > 0.f)) return fail(ENC_ERR_INVALID, "layernorm: eps must be positive");
   hipError_t e = enc::layernorm_bf16(static_cast<const enc::bf16_t*>(x), static_cast<const enc::bf16_t*>(gamma),
                                      static_cast<const enc::bf16_t*>(beta), static_cast<enc::bf16_t*>(y), rows,
@@ -185,7 +188,9 @@ int attention_entry(bool exact, const void* q, const void* k, const void* v_t, v
     return fail(ENC_ERR_INVALID, "attention: bad shape");
   if (batch == 0 || seq_len == 0) return ok();
   if (!q || !k || !v_t || !context) return fail(ENC_ERR_INVALID, "attention: null tensor pointer");
-  if (head_dim != 64) return fail(ENC_ERR_UNSUPPORTED, "attention: head_dim must be 64");
+  if (exact ? !(head_dim == 32 || head_dim == 64 || head_dim == 128) : head_dim != 64)
+    return fail(ENC_ERR_UNSUPPORTED, exact ? "attention: head_dim must be 32, 64 or 128"
+                                           : "online attention: head_dim must be 64");
   if (kv_len && key_mask) return fail(ENC_ERR_INVALID, "attention: pass kv_len or key_mask, not both");
   if (!(scale > 0.f)) return fail(ENC_ERR_INVALID, "attention: scale must be positive");
   if (exact && !enc::attention_seq_supported(seq_len))

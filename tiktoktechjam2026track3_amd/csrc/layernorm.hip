@@ -69,28 +69,32 @@ __device__ __forceinline__ Welford shfl_down(Welford s, int off) {
           __shfl_down(s.count, off, kWave)};
 }
 
-// VPT = width / 64 elements per lane; NV = vectors of 4 per virtual thread.
-template <int VPT>
+// WIDTH = row width; the row is WIDTH/4 vectors, lane l holds vectors
+// l + 64 s (s < SLOTS).  Narrow rows (WIDTH < 256) leave lanes and whole
+// virtual warps without a vector: their Welford states stay at count 0 and
+// still take part in the merges, as the idle threads of the reference's
+// 256-thread block do.
+template <int WIDTH>
 __global__ void __launch_bounds__(kRowsPerBlock * kWave)
 layernorm_kernel(const bf16_t* __restrict__ x, const bf16_t* __restrict__ gamma,
                  const bf16_t* __restrict__ beta, bf16_t* __restrict__ y, int64_t rows, float eps,
                  const uint8_t* __restrict__ row_mask) {
-  constexpr int kWidth = VPT * kWave;
-  constexpr int kVecs = kWidth / 4;
-  // vectors handled by virtual thread t: t + 256*k < kVecs; lane l holds t = l + 64w
-  constexpr int kSlots = VPT / 4;  // vectors per lane = (kVecs / 64)
+  constexpr int kVecs = WIDTH / 4;
+  constexpr int kSlots = kVecs < kWave ? 1 : kVecs / kWave;  // vectors per lane
   const int lane = threadIdx.x % kWave;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + threadIdx.x / kWave;
   if (row >= rows) return;
-  const bf16_t* xr = x + row * kWidth;
-  bf16_t* yr = y + row * kWidth;
+  const bf16_t* xr = x + row * WIDTH;
+  bf16_t* yr = y + row * WIDTH;
+  const bool has = kVecs >= kWave || lane < kVecs;  // this lane holds vectors
 
   // slot s <-> vector index v = lane + 64*s, i.e. virtual thread t = v % 256
   // (virtual warp w = (v / 64) % 4) and its (v / 256)-th vector.
   float v[kSlots][4];
 #pragma unroll
   for (int s = 0; s < kSlots; ++s) {
-    const u32x2 w = *reinterpret_cast<const u32x2*>(xr + (lane + kWave * s) * 4);
+    u32x2 w = {0u, 0u};
+    if (has) w = *reinterpret_cast<const u32x2*>(xr + (lane + kWave * s) * 4);
     v[s][0] = lo_bf16(w[0]);
     v[s][1] = hi_bf16(w[0]);
     v[s][2] = lo_bf16(w[1]);
@@ -98,9 +102,11 @@ layernorm_kernel(const bf16_t* __restrict__ x, const bf16_t* __restrict__ gamma,
   }
 
   if (row_mask != nullptr && row_mask[row] == 0) {
+    if (has) {
 #pragma unroll
-    for (int s = 0; s < kSlots; ++s)
-      *reinterpret_cast<u32x2*>(yr + (lane + kWave * s) * 4) = u32x2{0u, 0u};
+      for (int s = 0; s < kSlots; ++s)
+        *reinterpret_cast<u32x2*>(yr + (lane + kWave * s) * 4) = u32x2{0u, 0u};
+    }
     return;
   }
 
@@ -108,11 +114,13 @@ layernorm_kernel(const bf16_t* __restrict__ x, const bf16_t* __restrict__ gamma,
   Welford st[4];
 #pragma unroll
   for (int w = 0; w < 4; ++w) st[w] = {0.f, 0.f, 0.f};
+  if (has) {
 #pragma unroll
-  for (int s = 0; s < kSlots; ++s) {
-    const int w = s % 4;  // vector v = lane + 64 s belongs to virtual warp s % 4
+    for (int s = 0; s < kSlots; ++s) {
+      const int w = s % 4;  // vector v = lane + 64 s belongs to virtual warp s % 4
 #pragma unroll
-    for (int e = 0; e < 4; ++e) st[w] = welford_add(st[w], v[s][e]);
+      for (int e = 0; e < 4; ++e) st[w] = welford_add(st[w], v[s][e]);
+    }
   }
   // shuffle-down trees of the four virtual warps (lane 0 holds each result)
 #pragma unroll
@@ -125,9 +133,10 @@ layernorm_kernel(const bf16_t* __restrict__ x, const bf16_t* __restrict__ gamma,
   const Welford w1 = welford_merge(st[1], st[3]);
   w0 = welford_merge(w0, w1);
   const float mean = __shfl(w0.mean, 0, kWave);
-  const float var = __shfl(w0.m2, 0, kWave) / static_cast<float>(kWidth);
+  const float var = __shfl(w0.m2, 0, kWave) / static_cast<float>(WIDTH);
   const float rstd = rsqrtf(var + eps);
 
+  if (!has) return;
 #pragma unroll
   for (int s = 0; s < kSlots; ++s) {
     const int base = (lane + kWave * s) * 4;
@@ -142,11 +151,11 @@ layernorm_kernel(const bf16_t* __restrict__ x, const bf16_t* __restrict__ gamma,
   }
 }
 
-template <int VPT>
+template <int WIDTH>
 hipError_t launch_ln(const bf16_t* x, const bf16_t* g, const bf16_t* b, bf16_t* y,
                      int64_t rows, float eps, const uint8_t* mask, hipStream_t st) {
   const int64_t blocks = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
-  hipLaunchKernelGGL(layernorm_kernel<VPT>, dim3(static_cast<uint32_t>(blocks)),
+  hipLaunchKernelGGL(layernorm_kernel<WIDTH>, dim3(static_cast<uint32_t>(blocks)),
                      dim3(kRowsPerBlock * kWave), 0, st, x, g, b, y, rows, eps, mask);
   return hipGetLastError();
 }
@@ -154,7 +163,8 @@ hipError_t launch_ln(const bf16_t* x, const bf16_t* g, const bf16_t* b, bf16_t* 
 }  // namespace
 
 bool layernorm_supported(int64_t width) {
-  return width == 256 || width == 512 || width == 1024 || width == 2048 || width == 4096;
+  return width == 32 || width == 64 || width == 128 || width == 256 || width == 512 || width == 1024 ||
+         width == 2048 || width == 4096;
 }
 
 hipError_t layernorm_bf16(const bf16_t* x, const bf16_t* gamma, const bf16_t* beta, bf16_t* y,
@@ -162,11 +172,14 @@ hipError_t layernorm_bf16(const bf16_t* x, const bf16_t* gamma, const bf16_t* be
                           hipStream_t stream) {
   if (rows == 0) return hipSuccess;
   switch (width) {
-    case 256: return launch_ln<4>(x, gamma, beta, y, rows, eps, row_mask, stream);
-    case 512: return launch_ln<8>(x, gamma, beta, y, rows, eps, row_mask, stream);
-    case 1024: return launch_ln<16>(x, gamma, beta, y, rows, eps, row_mask, stream);
-    case 2048: return launch_ln<32>(x, gamma, beta, y, rows, eps, row_mask, stream);
-    case 4096: return launch_ln<64>(x, gamma, beta, y, rows, eps, row_mask, stream);
+    case 32: return launch_ln<32>(x, gamma, beta, y, rows, eps, row_mask, stream);
+    case 64: return launch_ln<64>(x, gamma, beta, y, rows, eps, row_mask, stream);
+    case 128: return launch_ln<128>(x, gamma, beta, y, rows, eps, row_mask, stream);
+    case 256: return launch_ln<256>(x, gamma, beta, y, rows, eps, row_mask, stream);
+    case 512: return launch_ln<512>(x, gamma, beta, y, rows, eps, row_mask, stream);
+    case 1024: return launch_ln<1024>(x, gamma, beta, y, rows, eps, row_mask, stream);
+    case 2048: return launch_ln<2048>(x, gamma, beta, y, rows, eps, row_mask, stream);
+    case 4096: return launch_ln<4096>(x, gamma, beta, y, rows, eps, row_mask, stream);
     default: return hipErrorInvalidValue;
   }
 }

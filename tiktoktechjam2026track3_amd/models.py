@@ -444,10 +444,14 @@ class UserOptimizedTransformer(BaselineTransformer):
             raise ValueError(f"expected x of shape [B, S, {cfg.d_model}], got {tuple(x.shape)}")
         hd = cfg.d_model // cfg.num_heads
         problems = []
-        if hd != 64:
-            problems.append(f"head_dim {hd} (supported: 64)")
-        if cfg.d_model not in (256, 512, 1024, 2048, 4096):
-            problems.append(f"d_model {cfg.d_model} (supported: powers of two 256..4096)")
+        if self.online_attention and hd != 64:
+            problems.append(f"head_dim {hd} (online attention supports 64)")
+        elif hd not in (32, 64, 128):
+            problems.append(f"head_dim {hd} (supported: 32, 64, 128)")
+        if cfg.d_model not in (32, 64, 128, 256, 512, 1024, 2048, 4096):
+            problems.append(f"d_model {cfg.d_model} (supported: powers of two 32..4096)")
+        if cfg.d_model % 64 != 0:
+            problems.append(f"d_model {cfg.d_model} (the projections need a multiple of 64)")
         seq_len = x.shape[1]
         if not self.online_attention and seq_len > 2048 and seq_len % 4:
             problems.append(
