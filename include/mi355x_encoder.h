@@ -103,7 +103,7 @@ int enc_qkv_proj_bf16(const void* x, const void* weight, const void* bias,
  * key_mask[b, j] == 0.  With kv_len, query rows i >= kv_len[b] are padding and
  * are written as zeros.  A query row with no allowed key is written as zeros.
  * context: [batch, seq_len, num_heads * head_dim] (token-major, the layout
- * out_proj consumes).  head_dim is 32, 64 or 128; v_t as produced by
+ * out_proj consumes).  head_dim is 8, 32, 64, 128 or 256; v_t as produced by
  * enc_qkv_proj_bf16.
  * Replaces transformer_benchmark/models.py:55-75 (baseline) and the
  * candidate's score/softmax/PV kernels: triangular_scores.py:110-291,

@@ -36,19 +36,19 @@ def test_cli_encoder_configs_c2_c3_pass_the_gate_with_profile(tmp_path):
     assert doc["environment"]["compute_units"] > 0
 
 
-def test_cli_official_cases_at_head_dims_32_64_128_pass(tmp_path):
-    """Official cases 2 (head dim 32), 9 (128), 10 (64) and 12 (32, 32 tokens)
-    with the reference runner's default gate and inputs."""
+def test_cli_official_cases_at_head_dims_8_to_256_pass(tmp_path):
+    """Official cases 2 (head dim 32), 8 (256), 9 (128), 10 (64), 11 (8) and
+    12 (32, 32 tokens) with the reference runner's default gate and inputs."""
     out = tmp_path / "official.json"
-    cmd = [sys.executable, "-u", str(ROOT / "torch_transformer_benchmark.py"), "--official-cases", "2", "9", "10",
-           "12", "--accuracy-trials", "2", "--warmup", "2", "--repeats", "5", "--benchmark-rounds", "1",
+    cmd = [sys.executable, "-u", str(ROOT / "torch_transformer_benchmark.py"), "--official-cases", "2", "8", "9",
+           "10", "11", "12", "--accuracy-trials", "2", "--warmup", "2", "--repeats", "5", "--benchmark-rounds", "1",
            "--json-output", str(out)]
     proc = subprocess.run(cmd, cwd=ROOT, capture_output=True, text=True, timeout=600)
     print(proc.stdout[-3000:], proc.stderr[-2000:], flush=True)
     assert proc.returncode == 0
     doc = json.loads(out.read_text())
     assert benchmarkctl_summary(doc) == {"mode": "official_matrix", "correctness_passed": True}
-    assert doc["requested_case_ids"] == [2, 9, 10, 12]
+    assert doc["requested_case_ids"] == [2, 8, 9, 10, 11, 12]
     for case in doc["cases"]:
         assert case["status"] == "succeeded"
         assert case["accuracy"]["failed_elements"] == 0

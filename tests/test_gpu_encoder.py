@@ -59,14 +59,15 @@ def test_encoder_parity(device, name):
 
 
 # Official cases the kernels cover: d_model 128 at head dims 32 (1-6, 12, 13),
-# 128 (9) and 64 (10).  Case 14 is c5's shape (the slow test below); cases 7
-# and 11 (head dim 8) and 8 (head dim 256) are rejected as unsupported.
-OFFICIAL_COVERED = (1, 2, 3, 4, 5, 6, 9, 10, 12, 13)
+# 128 (9), 64 (10) and 8 (11), and d_model 1024 at head dim 256 (8).  Case 14
+# is c5's shape (the slow test below).  Case 7 (d_model 32) is rejected as
+# unsupported: the projections need multiples of 64.
+OFFICIAL_COVERED = (1, 2, 3, 4, 5, 6, 8, 9, 10, 11, 12, 13)
 
 
 @pytest.mark.parametrize("case_id", OFFICIAL_COVERED)
 def test_encoder_parity_official_cases(device, case_id):
-    """Four causal layers at d_model 128 / ffn 128 against the oracle, on the
+    """Four causal layers at the case's shape against the oracle, on the
     reference runner's default input (seed 1234, no padding) and on a padded
     variant; the bitwise share is printed for the record."""
     cfg = OFFICIAL_TEST_CASES[case_id - 1]

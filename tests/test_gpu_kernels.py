@@ -342,31 +342,40 @@ def test_attention_config_shapes_bitwise(device, b, h, s, causal, prefix):
 
 
 @pytest.mark.parametrize(
-    "hd,b,h,s,causal,prefix",
+    "hd,b,h,s,causal,prefix,exact",
     [
-        (32, 64, 4, 128, True, True),  # official cases 1-6 (d_model 128, 4 heads)
-        (32, 1, 4, 128, False, False),
-        (32, 64, 4, 32, True, True),  # official case 12
-        (32, 8, 4, 1024, True, True),  # official case 13's rows
-        (32, 2, 3, 300, False, True),
-        (32, 1, 2, 4100, True, False),  # block-softmax regime
-        (128, 64, 1, 128, True, True),  # official case 9 (1 head of 128)
-        (128, 2, 2, 200, False, False),
-        (128, 1, 2, 1000, True, True),
-        (128, 1, 1, 4100, False, False),
-        (64, 64, 2, 128, True, True),  # official case 10 (2 heads of 64)
+        (32, 64, 4, 128, True, True, True),  # official cases 1-6 (d_model 128, 4 heads)
+        (32, 1, 4, 128, False, False, True),
+        (32, 64, 4, 32, True, True, True),  # official case 12
+        (32, 8, 4, 1024, True, True, True),  # official case 13's rows
+        (32, 2, 3, 300, False, True, True),
+        (32, 1, 2, 4100, True, False, False),  # block-softmax regime
+        (128, 64, 1, 128, True, True, True),  # official case 9 (1 head of 128)
+        (128, 2, 2, 200, False, False, True),
+        (128, 1, 2, 1000, True, True, True),
+        (128, 1, 1, 4100, False, False, True),
+        (64, 64, 2, 128, True, True, True),  # official case 10 (2 heads of 64)
+        (8, 64, 16, 128, True, True, True),  # official case 11 (16 heads of 8)
+        (8, 64, 4, 128, True, True, True),  # official case 7's attention (d_model 32)
+        (8, 2, 3, 300, False, True, False),
+        (8, 1, 2, 4100, True, False, False),
+        (256, 64, 4, 128, True, True, True),  # official case 8 (4 heads of 256)
+        (256, 2, 2, 200, False, False, True),
+        (256, 1, 2, 1000, True, True, True),
+        (256, 1, 1, 4100, False, False, True),
     ],
 )
-def test_attention_head_dims_bitwise(device, hd, b, h, s, causal, prefix):
-    """Head dims 32 and 128 at the official matrix's shapes (and the row
-    regimes either side of 2048 keys): with the scale hd^-0.5, which is not a
-    power of two for either, the context equals the oracle's bit for bit.
+def test_attention_head_dims_bitwise(device, hd, b, h, s, causal, prefix, exact):
+    """Head dims 8, 32, 128 and 256 at the official matrix's shapes (and the row
+    regimes either side of 2048 keys): with the scale hd^-0.5 (a power of two
+    only for 256), the context equals the oracle's bit for bit.
 
-    One measured exception: at head dim 32 with rows of more than 2048 keys
-    (no configuration or official case has them) the reference's P.V product
-    (N = 32) reduces K in a different order at some lengths (2560 and 4100
-    keys, not 4096); about 2 in 10^4 context values then differ by one bf16
-    ulp.  That case is held to the strict gate and a 99.9% bitwise share."""
+    Measured exceptions (exact=False), none at an official shape: for head
+    dims 8 and 32 the reference's P.V product (N = 8 or 32) reduces K in
+    another order at some lengths (300 keys at head dim 8; 2560 and 4100 keys,
+    not 4096, at head dim 32), and a few context values per 10^4 then differ
+    by one bf16 ulp.  Those cases are held to the strict gate and a 99.9%
+    bitwise share."""
     q, k, v, v_t = _attention_inputs(device, b, h, s, 5 * s + hd + b, hd=hd)
     kv_len = mask = None
     if prefix:
@@ -376,14 +385,14 @@ def test_attention_head_dims_bitwise(device, hd, b, h, s, causal, prefix):
         kv_len = lengths.int()
     out = native.attention(q, k, v_t, hd**-0.5, causal, kv_len=kv_len)
     ref = _oracle_context(q, k, v, causal, mask)
-    if hd == 32 and s > 2048:
-        assert strict_gate(ref, out) == 0 and bitwise_fraction(ref, out) > 0.999
-    elif mask is not None:
-        valid = mask[..., None].expand_as(out)
+    valid = torch.ones_like(out, dtype=torch.bool) if mask is None else mask[..., None].expand_as(out)
+    print(f"[attention hd {hd}] bitwise share {bitwise_fraction(ref[valid], out[valid]):.6f}", flush=True)
+    if exact:
         assert torch.equal(ref[valid], out[valid]), f"max abs {_context_error(ref[valid], out[valid])}"
-        assert torch.all(out[~valid] == 0)
     else:
-        assert torch.equal(ref, out), f"max abs {_context_error(ref, out)}"
+        assert strict_gate(ref[valid], out[valid]) == 0
+        assert bitwise_fraction(ref[valid], out[valid]) > 0.999
+    assert torch.all(out[~valid] == 0)
     if causal:
         assert torch.equal(out[:, 0, :].view(b, h, hd), v[:, :, 0, :])
 

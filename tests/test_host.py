@@ -180,15 +180,15 @@ def test_graph_replay_returns_independent_outputs():
 
 
 def test_native_path_rejects_shapes_the_kernels_do_not_cover():
-    config = TransformerConfig(1, 8, 128, 16, 128, 1, False)  # head_dim 8
+    config = TransformerConfig(1, 8, 128, 8, 128, 1, False)  # head_dim 16
     model = UserOptimizedTransformer(config)
-    with pytest.raises(UnsupportedShapeError, match="head_dim 8"):
+    with pytest.raises(UnsupportedShapeError, match="head_dim 16"):
         model._check_native_supported(torch.zeros(1, 8, 128, dtype=torch.bfloat16))
     narrow = UserOptimizedTransformer(TransformerConfig(1, 8, 32, 4, 32, 1, False))  # d_model 32
     with pytest.raises(UnsupportedShapeError, match="multiple of 64"):
         narrow._check_native_supported(torch.zeros(1, 8, 32, dtype=torch.bfloat16))
-    # head dims 32 and 128 are covered (official cases 1-6, 9, 12, 13)
-    for heads in (4, 1):
+    # head dims 32, 128 and 8 are covered (official cases 1-6, 9, 11, 12, 13)
+    for heads in (4, 1, 16):
         UserOptimizedTransformer(TransformerConfig(1, 8, 128, heads, 128, 1, True))._check_native_supported(
             torch.zeros(1, 8, 128, dtype=torch.bfloat16))
     with pytest.raises(UnsupportedShapeError, match="bfloat16"):

@@ -119,7 +119,7 @@ def test_matrix_classifies_out_of_memory_and_unsupported_shapes(tmp_path, monkey
         calls.append(config)
         if len(calls) == 1:
             raise RuntimeError("HIP out of memory. Tried to allocate 12.00 GiB")
-        raise UnsupportedShapeError("unsupported encoder shape: head_dim 8 (supported: 32, 64, 128)")
+        raise UnsupportedShapeError("unsupported encoder shape: head_dim 16 (supported: 8, 32, 64, 128, 256)")
 
     monkeypatch.setattr(runner, "_run_benchmark_case_with_profile", fake_case)
     args = runner.parse_args(["--official-cases", "14", "2", "--device", "cpu", "--json-output", str(out)])

@@ -26,9 +26,11 @@ SOURCES = (
     "layernorm.hip",
     "gemm.hip",
     "attention.hip",
+    "attention_hd8.hip",
     "attention_hd32.hip",
     "attention_hd64.hip",
     "attention_hd128.hip",
+    "attention_hd256.hip",
     "flash_attention.hip",
     "capi.hip",
 )
@@ -55,9 +57,11 @@ COMMON_FLAGS = (
 # v_accvgpr_read per score.  The GEMM keeps the compiler's choice: its large
 # accumulator tiles live in AGPRs.
 EXTRA_FLAGS = {
+    "attention_hd8.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form"),
     "attention_hd32.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form"),
     "attention_hd64.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form"),
     "attention_hd128.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form"),
+    "attention_hd256.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form"),
     "flash_attention.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form"),
 }
 

@@ -1,8 +1,7 @@
 // Exact attention entry (head-dim dispatch), the key-mask length kernel and
 // the expf self-check.  The exact attention kernel itself is a template over
 // the head dim (attention_exact.h), instantiated once per head dim in
-// attention_hd32.hip, attention_hd64.hip and attention_hd128.hip so the three
-// compile in parallel.
+// attention_hd{8,32,64,128,256}.hip so they compile in parallel.
 #include "attention_exact.h"
 
 namespace enc {
@@ -61,12 +60,16 @@ hipError_t attention_fwd_bf16(const bf16_t* q, const bf16_t* k, const bf16_t* v_
                               hipStream_t stream) {
   if (batch == 0 || seq_len == 0) return hipSuccess;
   switch (head_dim) {
+    case 8:
+      return attention_exact_hd8(q, k, v_t, ctx, batch, heads, seq_len, scale, kv_len, key_mask, causal, stream);
     case 32:
       return attention_exact_hd32(q, k, v_t, ctx, batch, heads, seq_len, scale, kv_len, key_mask, causal, stream);
     case 64:
       return attention_exact_hd64(q, k, v_t, ctx, batch, heads, seq_len, scale, kv_len, key_mask, causal, stream);
     case 128:
       return attention_exact_hd128(q, k, v_t, ctx, batch, heads, seq_len, scale, kv_len, key_mask, causal, stream);
+    case 256:
+      return attention_exact_hd256(q, k, v_t, ctx, batch, heads, seq_len, scale, kv_len, key_mask, causal, stream);
     default:
       return hipErrorInvalidValue;
   }

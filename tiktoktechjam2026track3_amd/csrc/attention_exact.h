@@ -1,5 +1,5 @@
-// Streaming multi-head attention forward for gfx950, head_dim 32, 64 or 128,
-// bitwise
+// Streaming multi-head attention forward for gfx950, head_dim 8, 32, 64, 128
+// or 256, bitwise
 // equal to the reference's materialised softmax attention.
 //
 // Scores are never materialised: each workgroup owns BQ = NW * 32 query rows
@@ -104,14 +104,18 @@ attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
                      const bf16_t* __restrict__ Vt, bf16_t* __restrict__ ctx, int H, int S,
                      int ld_vt, int num_qblocks, float scale,
                      const int32_t* __restrict__ kv_len, const uint8_t* __restrict__ key_mask) {
-  static_assert(HD == 32 || HD == 64 || HD == 128, "head_dim 32, 64 or 128");
-  static_assert(HD % (8 * NW) == 0, "each wavefront issues whole tile loads");
+  static_assert(HD == 8 || HD == 32 || HD == 64 || HD == 128 || HD == 256, "head_dim 8, 32, 64, 128 or 256");
   constexpr int kThreads = NW * kWave;
   constexpr int kBQ = NW * 32;
   constexpr int kTileElems = kBKV * HD;  // one K or V^T tile, bf16 elements
   constexpr int kChunksK = HD / 8;       // 16-byte chunks per K row
-  constexpr int kKSteps = HD / 16;       // 16-deep MFMA steps of q.k
-  constexpr int kDBlocks = HD / 32;      // 32-channel blocks of the context
+  // 16-deep MFMA steps of q.k.  Head dim 8 runs one step whose upper 8
+  // reduction lanes (lane half 1) hold zeros in both operands.
+  constexpr int kKSteps = HD < 16 ? 1 : HD / 16;
+  // 32-channel blocks of the context.  Head dim 8 uses MFMA rows 0..7 of one
+  // block; the other rows read V^T rows modulo 8 and are never written.
+  constexpr int kDBlocks = HD < 32 ? 1 : HD / 32;
+  constexpr int kSlabs = HD / 8;  // 1 KiB load instructions per K (or V^T) tile
   // K, V^T and key-mask tiles live in dynamic LDS sized at launch
   // (attn_lds_bytes): a static __shared__ array whose size depends on a
   // template parameter loses the kernel's host launch stub in this compiler.
@@ -164,9 +168,13 @@ attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
   if (MASK == kMaskPrefix && q0 >= kv_limit) {
     // Whole query tile is padding: zeros, no work.
     if (qrow < S) {
+      if constexpr (HD >= 16) {
 #pragma unroll
-      for (int c = 0; c < HD / 16; ++c)
-        *reinterpret_cast<u32x4*>(ctx_row + lhi * (HD / 2) + c * 8) = u32x4{0, 0, 0, 0};
+        for (int c = 0; c < HD / 16; ++c)
+          *reinterpret_cast<u32x4*>(ctx_row + lhi * (HD / 2) + c * 8) = u32x4{0, 0, 0, 0};
+      } else {
+        *reinterpret_cast<u32x2*>(ctx_row + lhi * 4) = u32x2{0u, 0u};
+      }
     }
     return;
   }
@@ -186,7 +194,7 @@ attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
   bf16x8 qf[kKSteps];
 #pragma unroll
   for (int ks = 0; ks < kKSteps; ++ks) {
-    if (qrow < S) {
+    if (qrow < S && (HD >= 16 || lhi == 0)) {
       qf[ks] = *reinterpret_cast<const bf16x8*>(Qh + static_cast<int64_t>(qrow) * HD + ks * 16 + lhi * 8);
     } else {
 #pragma unroll
@@ -204,8 +212,9 @@ attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
   // slot L % 8.  Each lane fetches the chunk that its slot holds.
   auto issue_full = [&](int buf, int k0, bool with_v) {
 #pragma unroll
-    for (int j = 0; j < HD / (8 * NW); ++j) {
+    for (int j = 0; j < (kSlabs + NW - 1) / NW; ++j) {
       const int slab = NW * j + wave;
+      if (kSlabs % NW != 0 && slab >= kSlabs) break;  // uniform per wavefront
       const int rk0 = (kWave / kChunksK) * slab;
       const int rk = rk0 + lane / kChunksK;
       const int ck = (lane % kChunksK) ^ (rk & ((kChunksK < 8 ? kChunksK : 8) - 1));
@@ -313,8 +322,9 @@ attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
     for (int ks = 0; ks < kKSteps; ++ks) {
 #pragma unroll
       for (int kb32 = 0; kb32 < 2; ++kb32) {
-        const bf16x8 kf =
-            *reinterpret_cast<const bf16x8*>(&sK[buf * kTileElems + k_off<HD>(kb32 * 32 + krow, 2 * ks + lhi)]);
+        const int chunk = HD >= 16 ? 2 * ks + lhi : 0;
+        bf16x8 kf = *reinterpret_cast<const bf16x8*>(&sK[buf * kTileElems + k_off<HD>(kb32 * 32 + krow, chunk)]);
+        if (HD < 16 && lhi != 0) kf = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
         s[kb32] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], s[kb32], 0, 0, 0);
       }
     }
@@ -608,7 +618,8 @@ attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
     for (int kk = 0; kk < 4; ++kk) {
 #pragma unroll
       for (int db = 0; db < kDBlocks; ++db) {
-        const bf16x8 vf = *reinterpret_cast<const bf16x8*>(&sV[buf * kTileElems + v_off(db * 32 + l32, 2 * kk + lhi)]);
+        const int vrow = HD >= 32 ? db * 32 + l32 : (l32 & (HD - 1));
+        const bf16x8 vf = *reinterpret_cast<const bf16x8*>(&sV[buf * kTileElems + v_off(vrow, 2 * kk + lhi)]);
         o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[kk], o[db], 0, 0, 0);
       }
     }
@@ -632,7 +643,7 @@ attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
 #pragma unroll
     for (int db = 0; db < kDBlocks; ++db) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < (HD < 32 ? HD / 8 : 4); ++i) {
         const int d = db * 32 + 8 * i + 4 * lhi;
         u32x2 w = {0u, 0u};
         if (!zero) {
@@ -680,19 +691,26 @@ hipError_t dispatch_order(const bf16_t* q, const bf16_t* k, const bf16_t* vt, bf
     return launch_attn<HD, 4, CAUSAL, MASK, POW2, true>(q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
   // Small problems use one-wavefront workgroups (32 queries) so more of the
   // 256 CUs get work; larger ones share each K/V tile among 4 wavefronts.
-  // Rows of at most 256 keys keep every tile resident in LDS.
+  // Rows of at most 256 keys keep every tile resident in LDS (at most 128 keys
+  // for head dim 256, whose four resident tiles would exceed the 160 KiB of
+  // LDS of a CU).
+  constexpr bool kRes4 = attn_lds_bytes(HD, 4) <= 160 * 1024;
   const int64_t groups128 = static_cast<int64_t>(B) * H * ((S + 127) / 128);
   if (groups128 < 512) {
     if (S <= 2 * kBKV)
       return launch_attn<HD, 1, CAUSAL, MASK, POW2, false, 2>(q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
-    if (S <= 4 * kBKV)
-      return launch_attn<HD, 1, CAUSAL, MASK, POW2, false, 4>(q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
+    if constexpr (kRes4) {
+      if (S <= 4 * kBKV)
+        return launch_attn<HD, 1, CAUSAL, MASK, POW2, false, 4>(q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
+    }
     return launch_attn<HD, 1, CAUSAL, MASK, POW2, false>(q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
   }
   if (S <= 2 * kBKV)
     return launch_attn<HD, 4, CAUSAL, MASK, POW2, false, 2>(q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
-  if (S <= 4 * kBKV)
-    return launch_attn<HD, 4, CAUSAL, MASK, POW2, false, 4>(q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
+  if constexpr (kRes4) {
+    if (S <= 4 * kBKV)
+      return launch_attn<HD, 4, CAUSAL, MASK, POW2, false, 4>(q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
+  }
   return launch_attn<HD, 4, CAUSAL, MASK, POW2, false>(q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
 }
 
@@ -702,7 +720,7 @@ hipError_t dispatch_pow2(bool pow2, const bf16_t* q, const bf16_t* k, const bf16
                          const uint8_t* key_mask, hipStream_t st) {
   // The general path evaluates bf16(bf16(q.k) * scale) literally, which is
   // exact for every scale; the power-of-two variant only saves work.  Head
-  // dims other than 64 (scales 32^-0.5, 128^-0.5) instantiate the general one.
+  // dims other than 64 instantiate the general one only.
   if constexpr (HD == 64) {
     if (pow2) return dispatch_order<HD, CAUSAL, MASK, true>(q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
   }

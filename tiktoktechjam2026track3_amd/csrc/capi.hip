@@ -86,9 +86,9 @@ int check_encoder_shape(int64_t B, int64_t S, int64_t D, int64_t H, int64_t F, b
     return fail(ENC_ERR_INVALID, "batch, seq_len, d_model, num_heads and ffn_dim must be positive");
   if (D % H != 0) return fail(ENC_ERR_INVALID, "d_model must be divisible by num_heads");
   const int64_t hd = D / H;
-  if (exact_attention ? !(hd == 32 || hd == 64 || hd == 128) : hd != 64)
+  if (exact_attention ? !(hd == 8 || hd == 32 || hd == 64 || hd == 128 || hd == 256) : hd != 64)
     return fail(ENC_ERR_UNSUPPORTED,
-                std::string(exact_attention ? "attention kernel supports head_dim 32, 64 or 128"
+                std::string(exact_attention ? "attention kernel supports head_dim 8, 32, 64, 128 or 256"
                                             : "online attention kernel supports head_dim 64 only") +
                     " (got " + std::to_string(hd) + ")");
   if (!enc::layernorm_supported(D))
@@ -188,8 +188,9 @@ int attention_entry(bool exact, const void* q, const void* k, const void* v_t, v
     return fail(ENC_ERR_INVALID, "attention: bad shape");
   if (batch == 0 || seq_len == 0) return ok();
   if (!q || !k || !v_t || !context) return fail(ENC_ERR_INVALID, "attention: null tensor pointer");
-  if (exact ? !(head_dim == 32 || head_dim == 64 || head_dim == 128) : head_dim != 64)
-    return fail(ENC_ERR_UNSUPPORTED, exact ? "attention: head_dim must be 32, 64 or 128"
+  if (exact ? !(head_dim == 8 || head_dim == 32 || head_dim == 64 || head_dim == 128 || head_dim == 256)
+            : head_dim != 64)
+    return fail(ENC_ERR_UNSUPPORTED, exact ? "attention: head_dim must be 8, 32, 64, 128 or 256"
                                            : "online attention: head_dim must be 64");
   if (kv_len && key_mask) return fail(ENC_ERR_INVALID, "attention: pass kv_len or key_mask, not both");
   if (!(scale > 0.f)) return fail(ENC_ERR_INVALID, "attention: scale must be positive");

@@ -52,13 +52,16 @@ void gemm_pick_tile(int64_t M, int64_t N, int epilogue, int num_cus, int* bm, in
 // into partial (chunk index % split) and the partials are added in order.
 void gemm_split_plan(int64_t M, int64_t N, int64_t K, int* split, int* chunk);
 
-// Exact three-sweep attention (head_dim 32, 64 or 128), bit-exact with the
+// Exact three-sweep attention (head_dim 8, 32, 64, 128 or 256), bit-exact with the
 // reference's materialised softmax.  v_t row stride is ld_vt = round_up(S, 8).
 hipError_t attention_fwd_bf16(const bf16_t* q, const bf16_t* k, const bf16_t* v_t, bf16_t* ctx,
                               int batch, int heads, int seq_len, int head_dim, float scale,
                               bool causal, const int32_t* kv_len, const uint8_t* key_mask,
                               hipStream_t stream);
 // The per-head-dim instantiations behind attention_fwd_bf16.
+hipError_t attention_exact_hd8(const bf16_t* q, const bf16_t* k, const bf16_t* v_t, bf16_t* ctx, int batch,
+                               int heads, int seq_len, float scale, const int32_t* kv_len,
+                               const uint8_t* key_mask, bool causal, hipStream_t stream);
 hipError_t attention_exact_hd32(const bf16_t* q, const bf16_t* k, const bf16_t* v_t, bf16_t* ctx, int batch,
                                 int heads, int seq_len, float scale, const int32_t* kv_len,
                                 const uint8_t* key_mask, bool causal, hipStream_t stream);
@@ -66,6 +69,9 @@ hipError_t attention_exact_hd64(const bf16_t* q, const bf16_t* k, const bf16_t* 
                                 int heads, int seq_len, float scale, const int32_t* kv_len,
                                 const uint8_t* key_mask, bool causal, hipStream_t stream);
 hipError_t attention_exact_hd128(const bf16_t* q, const bf16_t* k, const bf16_t* v_t, bf16_t* ctx, int batch,
+                                 int heads, int seq_len, float scale, const int32_t* kv_len,
+                                 const uint8_t* key_mask, bool causal, hipStream_t stream);
+hipError_t attention_exact_hd256(const bf16_t* q, const bf16_t* k, const bf16_t* v_t, bf16_t* ctx, int batch,
                                  int heads, int seq_len, float scale, const int32_t* kv_len,
                                  const uint8_t* key_mask, bool causal, hipStream_t stream);
 

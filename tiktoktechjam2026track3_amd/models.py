@@ -446,8 +446,8 @@ class UserOptimizedTransformer(BaselineTransformer):
         problems = []
         if self.online_attention and hd != 64:
             problems.append(f"head_dim {hd} (online attention supports 64)")
-        elif hd not in (32, 64, 128):
-            problems.append(f"head_dim {hd} (supported: 32, 64, 128)")
+        elif hd not in (8, 32, 64, 128, 256):
+            problems.append(f"head_dim {hd} (supported: 8, 32, 64, 128, 256)")
         if cfg.d_model not in (32, 64, 128, 256, 512, 1024, 2048, 4096):
             problems.append(f"d_model {cfg.d_model} (supported: powers of two 32..4096)")
         if cfg.d_model % 64 != 0:
