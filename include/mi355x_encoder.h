@@ -67,7 +67,7 @@ int enc_layernorm_bf16(const void* x, const void* gamma, const void* beta,
  * with bf16 MFMA and fp32 accumulation.  residual (same shape as out) is read
  * by the RESIDUAL epilogues only; row_mask (nullable, length rows) selects the
  * masked-row behaviour described at the ENC_EPI_* constants.
- * in_features % 64 == 0 and out_features % 64 == 0; rows is arbitrary.
+ * in_features % 32 == 0 and out_features % 32 == 0; rows is arbitrary.
  * Replaces nn.Linear + F.gelu + residual add at transformer_benchmark/models.py:
  * 76, 733-734 and the fused wrappers fused_ffn.py:91-126 (bias+GELU),
  * fused_ffn_out.py:89-132 (bias+residual), fused_attention_out.py:89-130

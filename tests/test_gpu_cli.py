@@ -54,12 +54,20 @@ def test_cli_official_cases_at_head_dims_8_to_256_pass(tmp_path):
         assert case["accuracy"]["failed_elements"] == 0
 
 
-def test_cli_official_case_with_unsupported_head_dim_is_an_execution_failure(tmp_path):
+def test_cli_remaining_official_cases_1_to_13_pass(tmp_path):
+    """With the test above, cases 1-13 of the official matrix through the CLI:
+    1, 3-6 and 13 (head dim 32 at 1 to 10000 sequences and 1024 tokens) and 7
+    (d_model 32, head dim 8).  Case 14 is c5's shape, whose baseline cannot
+    materialise its scores; the encoder tests cover it."""
     out = tmp_path / "official.json"
-    cmd = [sys.executable, "-u", str(ROOT / "torch_transformer_benchmark.py"), "--official-cases", "7",
-           "--accuracy-trials", "1", "--json-output", str(out)]
+    cmd = [sys.executable, "-u", str(ROOT / "torch_transformer_benchmark.py"), "--official-cases", "1", "3", "4",
+           "5", "6", "7", "13", "--accuracy-trials", "1", "--warmup", "2", "--repeats", "3", "--benchmark-rounds",
+           "1", "--json-output", str(out)]
     proc = subprocess.run(cmd, cwd=ROOT, capture_output=True, text=True, timeout=600)
-    assert proc.returncode == 3, proc.stdout[-2000:] + proc.stderr[-2000:]
+    print(proc.stdout[-3000:], proc.stderr[-2000:], flush=True)
+    assert proc.returncode == 0
     doc = json.loads(out.read_text())
-    benchmarkctl_summary(doc)
-    assert doc["cases"][0]["failure_category"] == "unsupported_shape"
+    assert benchmarkctl_summary(doc) == {"mode": "official_matrix", "correctness_passed": True}
+    for case in doc["cases"]:
+        assert case["status"] == "succeeded"
+        assert case["accuracy"]["failed_elements"] == 0

@@ -58,11 +58,10 @@ def test_encoder_parity(device, name):
         assert torch.all(out[~mask] == 0)
 
 
-# Official cases the kernels cover: d_model 128 at head dims 32 (1-6, 12, 13),
-# 128 (9), 64 (10) and 8 (11), and d_model 1024 at head dim 256 (8).  Case 14
-# is c5's shape (the slow test below).  Case 7 (d_model 32) is rejected as
-# unsupported: the projections need multiples of 64.
-OFFICIAL_COVERED = (1, 2, 3, 4, 5, 6, 8, 9, 10, 11, 12, 13)
+# Official cases: d_model 128 at head dims 32 (1-6, 12, 13), 128 (9), 64 (10)
+# and 8 (11); d_model 32 at head dim 8 (7); d_model 1024 at head dim 256 (8).
+# Case 14 is c5's shape (the slow test below).
+OFFICIAL_COVERED = (1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13)
 
 
 @pytest.mark.parametrize("case_id", OFFICIAL_COVERED)

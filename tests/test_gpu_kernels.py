@@ -180,6 +180,25 @@ def test_linear_residual(device, m, n, k, epi):
     assert within_composite(ref, out2, y, 1.0)
 
 
+@pytest.mark.parametrize(
+    "m,n,k",
+    [(8192, 96, 32), (8192, 32, 32), (37, 96, 32), (1, 32, 32), (300, 64, 96), (8192, 384, 128), (8192, 128, 128)],
+)
+def test_linear_narrow_and_d128_shapes_bitwise(device, m, n, k):
+    """The official matrix's projection shapes: d_model 32 (N or K not a
+    multiple of 64: the one-block-per-wavefront kernel) and d_model 128; every
+    epilogue equals torch's bf16 ops bit for bit."""
+    a, w, bias, res, _ = _linear_case(device, m, n, k, 29 * m + n + k)
+    ref = F.linear(a, w, bias)
+    assert torch.equal(native.linear(a, w, bias, native.ENC_EPI_BIAS), ref)
+    assert torch.equal(native.linear(a, w, bias, native.ENC_EPI_BIAS_GELU), F.gelu(ref, approximate="none"))
+    mask = torch.rand(m, device=device) > 0.3
+    out = native.linear(a, w, bias, native.ENC_EPI_BIAS_RESIDUAL_ZERO, residual=res, row_mask=mask)
+    assert torch.equal(out[mask], (res + ref)[mask]) and torch.all(out[~mask] == 0)
+    out = native.linear(a, w, bias, native.ENC_EPI_BIAS_RESIDUAL_KEEP, residual=res, row_mask=mask)
+    assert torch.equal(out[mask], (res + ref)[mask]) and torch.equal(out[~mask], res[~mask])
+
+
 @pytest.mark.parametrize("m,n,k", [(128, 512, 2048), (64, 512, 2048), (256, 512, 2048), (16, 1536, 512), (1, 512, 512), (16, 1024, 4096), (128, 1024, 4096)])
 def test_linear_split_k_order_bitwise(device, m, n, k):
     """Shapes where torch's bf16 nn.Linear splits K: the kernel's partial sums
@@ -191,7 +210,11 @@ def test_linear_split_k_order_bitwise(device, m, n, k):
     assert torch.equal(out_res, res + F.linear(a, w, bias))
 
 
-@pytest.mark.parametrize("b,s,d,h", [(1, 128, 512, 8), (2, 100, 512, 8), (8, 1024, 1024, 16), (3, 37, 1024, 16)])
+@pytest.mark.parametrize(
+    "b,s,d,h",
+    [(1, 128, 512, 8), (2, 100, 512, 8), (8, 1024, 1024, 16), (3, 37, 1024, 16), (64, 128, 32, 4), (3, 37, 128, 16),
+     (2, 100, 1024, 4)],
+)
 def test_qkv_head_major(device, b, s, d, h):
     g = torch.Generator(device=device).manual_seed(b * s + d)
     x = torch.randn(b, s, d, generator=g, device=device).bfloat16()

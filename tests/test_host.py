@@ -17,7 +17,7 @@ import pytest
 import torch
 
 from tiktoktechjam2026track3_amd import native, profiling
-from tiktoktechjam2026track3_amd.cases import TransformerConfig
+from tiktoktechjam2026track3_amd.cases import OFFICIAL_TEST_CASES, TransformerConfig
 from tiktoktechjam2026track3_amd.correctness import compare_outputs
 from tiktoktechjam2026track3_amd.models import (
     BaselineTransformer,
@@ -184,13 +184,14 @@ def test_native_path_rejects_shapes_the_kernels_do_not_cover():
     model = UserOptimizedTransformer(config)
     with pytest.raises(UnsupportedShapeError, match="head_dim 16"):
         model._check_native_supported(torch.zeros(1, 8, 128, dtype=torch.bfloat16))
-    narrow = UserOptimizedTransformer(TransformerConfig(1, 8, 32, 4, 32, 1, False))  # d_model 32
-    with pytest.raises(UnsupportedShapeError, match="multiple of 64"):
-        narrow._check_native_supported(torch.zeros(1, 8, 32, dtype=torch.bfloat16))
-    # head dims 32, 128 and 8 are covered (official cases 1-6, 9, 11, 12, 13)
-    for heads in (4, 1, 16):
-        UserOptimizedTransformer(TransformerConfig(1, 8, 128, heads, 128, 1, True))._check_native_supported(
-            torch.zeros(1, 8, 128, dtype=torch.bfloat16))
+    odd_ffn = UserOptimizedTransformer(TransformerConfig(1, 8, 128, 4, 48, 1, False))  # ffn_dim 48
+    with pytest.raises(UnsupportedShapeError, match="multiple of 32"):
+        odd_ffn._check_native_supported(torch.zeros(1, 8, 128, dtype=torch.bfloat16))
+    # every official case's shape is covered (head dims 8 to 256, d_model 32 to 1024)
+    for case in OFFICIAL_TEST_CASES:
+        small = TransformerConfig(1, 8, case.d_model, case.num_heads, case.ffn_dim, 1, case.causal)
+        UserOptimizedTransformer(small)._check_native_supported(
+            torch.zeros(1, 8, case.d_model, dtype=torch.bfloat16))
     with pytest.raises(UnsupportedShapeError, match="bfloat16"):
         model._check_native_supported(torch.zeros(1, 8, 128))
 

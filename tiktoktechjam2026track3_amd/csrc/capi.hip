@@ -97,8 +97,8 @@ int check_encoder_shape(int64_t B, int64_t S, int64_t D, int64_t H, int64_t F, b
   if (exact_attention && !enc::attention_seq_supported(S))
     return fail(ENC_ERR_UNSUPPORTED, "seq_len above 2048 must be a multiple of 4 (got " +
                                          std::to_string(S) + ")");
-  if (D % 64 != 0 || F % 64 != 0)
-    return fail(ENC_ERR_UNSUPPORTED, "d_model and ffn_dim must be multiples of 64");
+  if (D % 32 != 0 || F % 32 != 0)
+    return fail(ENC_ERR_UNSUPPORTED, "d_model and ffn_dim must be multiples of 32");
   if (B * S >= (int64_t(1) << 31)) return fail(ENC_ERR_UNSUPPORTED, "batch * seq_len must be < 2^31");
   return ENC_OK;
 }
@@ -138,7 +138,7 @@ int enc_linear_bf16(const void* a, const void* weight, const void* bias, const v
   const bool needs_res = epilogue == ENC_EPI_BIAS_RESIDUAL_KEEP || epilogue == ENC_EPI_BIAS_RESIDUAL_ZERO;
   if (needs_res && !residual) return fail(ENC_ERR_INVALID, "linear: residual epilogue needs a residual");
   if (!enc::gemm_supported(rows, out_features, in_features))
-    return fail(ENC_ERR_UNSUPPORTED, "linear: in_features and out_features must be multiples of 64 (got " +
+    return fail(ENC_ERR_UNSUPPORTED, "linear: in_features and out_features must be multiples of 32 (got " +
                                          std::to_string(in_features) + ", " + std::to_string(out_features) + ")");
   enc::GemmEpilogueArgs ep;
   ep.bias = static_cast<const enc::bf16_t*>(bias);
@@ -161,7 +161,7 @@ int enc_qkv_proj_bf16(const void* x, const void* weight, const void* bias, void*
   if (d_model % num_heads != 0) return fail(ENC_ERR_INVALID, "qkv: d_model must be divisible by num_heads");
   const int64_t M = batch * seq_len;
   if (!enc::gemm_supported(M, 3 * d_model, d_model))
-    return fail(ENC_ERR_UNSUPPORTED, "qkv: d_model must be a multiple of 64");
+    return fail(ENC_ERR_UNSUPPORTED, "qkv: d_model must be a multiple of 32");
   enc::GemmEpilogueArgs ep;
   ep.bias = static_cast<const enc::bf16_t*>(bias);
   ep.q = static_cast<enc::bf16_t*>(q);

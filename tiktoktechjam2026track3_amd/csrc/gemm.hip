@@ -282,6 +282,41 @@ gemm_bf16_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int
 
 
 // ---------------------------------------------------------------------------
+// Narrow-shape kernel, for N or K that is a multiple of 32 but not of 64
+// (d_model 32: K = 32, N = 32 or 96).  One wavefront per 32x32 output block;
+// the MFMA fragments come straight from global memory (lane (r = l % 32,
+// h = l / 32) loads the 16 bytes at K offset 16 ks + 8 h of A row r and of W
+// row r) and K accumulates sequentially in 16-deep MFMA steps, the order of
+// the unsplit kernels.  At these sizes neither LDS staging nor larger tiles
+// pay.
+template <int EPI>
+__global__ void __launch_bounds__(kThreads)
+gemm_narrow_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int M, int N, int K,
+                   GemmEpilogueArgs ep) {
+  const int lane = threadIdx.x % kWave;
+  const int l32 = lane & 31;
+  const int lhi = lane >> 5;
+  const int blocks_n = N / 32;
+  const int64_t blocks = static_cast<int64_t>((M + 31) / 32) * blocks_n;
+  const int64_t blk = static_cast<int64_t>(blockIdx.x) * (kThreads / kWave) + threadIdx.x / kWave;
+  if (blk >= blocks) return;  // uniform per wavefront; the kernel has no barrier
+  const int row0 = static_cast<int>(blk / blocks_n) * 32;
+  const int col0 = static_cast<int>(blk % blocks_n) * 32;
+  const int arow = min(row0 + l32, M - 1);  // rows past M re-load the last row, never stored
+  const bf16_t* a = A + static_cast<int64_t>(arow) * K + lhi * 8;
+  const bf16_t* w = W + static_cast<int64_t>(col0 + l32) * K + lhi * 8;
+  f32x16 acc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+  for (int k0 = 0; k0 < K; k0 += 16) {
+    const bf16x8 af = *reinterpret_cast<const bf16x8*>(a + k0);
+    const bf16x8 wf = *reinterpret_cast<const bf16x8*>(w + k0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, wf, acc, 0, 0, 0);
+  }
+  store_block<EPI>(ep, M, N, row0, col0, acc);
+}
+
+// ---------------------------------------------------------------------------
 // Large-tile kernel: BM x BN output tile (256x256, 256x128 or 128x128), four
 // wavefronts in a 2 x 2 grid, each owning a (BM/2) x (BN/2) sub-tile of 32x32
 // fp32 accumulator blocks (up to 256 registers per lane, held in AGPRs).
@@ -878,6 +913,27 @@ hipError_t launch_tile(const bf16_t* A, const bf16_t* W, int M, int N, int K, in
   return hipGetLastError();
 }
 
+hipError_t launch_narrow(const bf16_t* A, const bf16_t* W, int M, int N, int K, int epi,
+                         const GemmEpilogueArgs& ep, hipStream_t st) {
+  const int64_t blocks = static_cast<int64_t>((M + 31) / 32) * (N / 32);
+  const dim3 grid(static_cast<uint32_t>((blocks + kThreads / kWave - 1) / (kThreads / kWave))), block(kThreads);
+  switch (epi) {
+    case kEpiBias: hipLaunchKernelGGL(gemm_narrow_kernel<kEpiBias>, grid, block, 0, st, A, W, M, N, K, ep); break;
+    case kEpiBiasGelu: hipLaunchKernelGGL(gemm_narrow_kernel<kEpiBiasGelu>, grid, block, 0, st, A, W, M, N, K, ep); break;
+    case kEpiResidualKeep:
+      hipLaunchKernelGGL(gemm_narrow_kernel<kEpiResidualKeep>, grid, block, 0, st, A, W, M, N, K, ep);
+      break;
+    case kEpiResidualZero:
+      hipLaunchKernelGGL(gemm_narrow_kernel<kEpiResidualZero>, grid, block, 0, st, A, W, M, N, K, ep);
+      break;
+    case kEpiQkvHeadMajor:
+      hipLaunchKernelGGL(gemm_narrow_kernel<kEpiQkvHeadMajor>, grid, block, 0, st, A, W, M, N, K, ep);
+      break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 // K-split launches use the 64x64 tile: four partial accumulator sets still fit
 // the register budget there.
 template <int SPLIT, int CW>
@@ -989,7 +1045,7 @@ void gemm_pick_tile(int64_t M, int64_t N, int epilogue, int num_cus, int* bm, in
 }
 
 bool gemm_supported(int64_t M, int64_t N, int64_t K) {
-  return M >= 0 && N > 0 && K > 0 && N % 64 == 0 && K % 64 == 0 && M < (int64_t(1) << 31) &&
+  return M >= 0 && N > 0 && K > 0 && N % 32 == 0 && K % 32 == 0 && M < (int64_t(1) << 31) &&
          N < (int64_t(1) << 20) && K < (int64_t(1) << 20);
 }
 
@@ -997,6 +1053,9 @@ hipError_t gemm_bf16(const bf16_t* A, const bf16_t* W, int64_t M, int64_t N, int
                      const GemmEpilogueArgs& ep, int num_cus, hipStream_t stream) {
   if (M == 0) return hipSuccess;
   const int m = static_cast<int>(M), n = static_cast<int>(N), k = static_cast<int>(K);
+  // N or K not a multiple of 64: one 32x32 block per wavefront, sequential K
+  // (none of these shapes has a split rule)
+  if (N % 64 != 0 || K % 64 != 0) return launch_narrow(A, W, m, n, k, epi, ep, stream);
   int split, chunk;
   gemm_split_plan(M, N, K, &split, &chunk);
   const bool aligned16 = reinterpret_cast<uintptr_t>(A) % 16 == 0 && reinterpret_cast<uintptr_t>(W) % 16 == 0;

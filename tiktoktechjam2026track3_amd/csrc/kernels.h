@@ -40,7 +40,7 @@ hipError_t layernorm_bf16(const bf16_t* x, const bf16_t* gamma, const bf16_t* be
                           hipStream_t stream);
 
 // GEMM: C[M, N] = A[M, K] . W[N, K]^T with the given epilogue.
-// Requirements: N % 64 == 0, K % 64 == 0, M >= 0.
+// Requirements: N % 32 == 0, K % 32 == 0, M >= 0.
 bool gemm_supported(int64_t M, int64_t N, int64_t K);
 hipError_t gemm_bf16(const bf16_t* A, const bf16_t* W, int64_t M, int64_t N, int64_t K,
                      int epilogue, const GemmEpilogueArgs& ep, int num_cus, hipStream_t stream);

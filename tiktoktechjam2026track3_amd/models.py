@@ -450,15 +450,15 @@ class UserOptimizedTransformer(BaselineTransformer):
             problems.append(f"head_dim {hd} (supported: 8, 32, 64, 128, 256)")
         if cfg.d_model not in (32, 64, 128, 256, 512, 1024, 2048, 4096):
             problems.append(f"d_model {cfg.d_model} (supported: powers of two 32..4096)")
-        if cfg.d_model % 64 != 0:
-            problems.append(f"d_model {cfg.d_model} (the projections need a multiple of 64)")
+        if cfg.d_model % 32 != 0:
+            problems.append(f"d_model {cfg.d_model} (the projections need a multiple of 32)")
         seq_len = x.shape[1]
         if not self.online_attention and seq_len > 2048 and seq_len % 4:
             problems.append(
                 f"seq_len {seq_len} (exact attention above 2048 needs a multiple of 4)"
             )
-        if cfg.ffn_dim % 64 != 0:
-            problems.append(f"ffn_dim {cfg.ffn_dim} (must be a multiple of 64)")
+        if cfg.ffn_dim % 32 != 0:
+            problems.append(f"ffn_dim {cfg.ffn_dim} (must be a multiple of 32)")
         if problems:
             raise UnsupportedShapeError("unsupported encoder shape: " + ", ".join(problems))
 
