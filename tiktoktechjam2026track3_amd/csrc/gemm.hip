@@ -811,6 +811,34 @@ gemm_skinny_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, i
   };
 
   const int wrow = 16 + (SPLIT == 1 ? wave * 16 : 0) + l16;  // this lane's W row in the stage
+  // The epilogue's operands (bias, residual, row-mask bytes) do not depend on
+  // the product: they are loaded before the K loop, so their latency overlaps
+  // it instead of following the last MFMA.
+  const int col = n0 + (SPLIT == 1 ? wave * 16 : 0) + l16;
+  const float bias = bf16_to_f32(ep.bias[col]);
+  constexpr bool kResidual = EPI == kEpiResidualKeep || EPI == kEpiResidualZero;
+  // The values are held zero-extended in 32-bit registers and the mask
+  // bytes untested until the epilogue: packing or testing them here would
+  // make the wavefront wait for the loads before its K loop.
+  uint32_t res[4] = {0u, 0u, 0u, 0u};
+  uint32_t keep[4] = {1u, 1u, 1u, 1u};
+  if constexpr (kResidual) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int r = min(m0 + 4 * g + j, M - 1);
+      res[j] = ep.residual[static_cast<int64_t>(r) * N + col];
+    }
+    // without a mask the loads read the residual's first bytes (any valid
+    // address) and the select below ignores them; a branch around the loads
+    // would have the compiler test the bytes where the branch joins
+    const bool has_mask = ep.row_mask != nullptr;
+    const uint8_t* mask = has_mask ? ep.row_mask : reinterpret_cast<const uint8_t*>(ep.residual);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t byte = mask[has_mask ? min(m0 + 4 * g + j, M - 1) : 0];
+      keep[j] = has_mask ? byte : 1u;
+    }
+  }
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   const int nst = K / kSkinnyKS;
   issue_stage(0, 0);
@@ -835,7 +863,6 @@ gemm_skinny_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, i
     if (st + 2 < nst) issue_stage(buf, (st + 2) * kSkinnyKS);
   }
 
-  const int col = n0 + (SPLIT == 1 ? wave * 16 : 0) + l16;
   if constexpr (SPLIT > 1) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) red[wave][lane][j] = acc[j];
@@ -849,11 +876,21 @@ gemm_skinny_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, i
       acc[j] = sum;
     }
   }
-  const float bias = bf16_to_f32(ep.bias[col]);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int r = m0 + 4 * g + j;
-    if (r < M) store_one<EPI>(ep, N, r, col, acc[j], bias);
+    if (r >= M) continue;
+    if constexpr (kResidual) {
+      const int64_t idx = static_cast<int64_t>(r) * N + col;
+      const float y = round_bf16(acc[j] + bias);  // nn.Linear output boundary
+      if (keep[j] != 0u) {
+        ep.out[idx] = f32_to_bf16(__uint_as_float(res[j] << 16) + y);
+      } else {
+        ep.out[idx] = (EPI == kEpiResidualKeep) ? static_cast<bf16_t>(res[j]) : bf16_t(0);
+      }
+    } else {
+      store_one<EPI>(ep, N, r, col, acc[j], bias);
+    }
   }
 }
 
