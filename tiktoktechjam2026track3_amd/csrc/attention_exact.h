@@ -98,6 +98,12 @@ __device__ __forceinline__ int tile_key(int kb32, int r, int h) {
 // RES > 0: short rows (at most RES tiles): every K/V tile is loaded into LDS
 // once and the three sweeps read them from there, with no further loads or
 // barriers.  RES == 0: the two-stage ring streams the tiles for each sweep.
+// NW == 2 with RES == 2 (key split): the two wavefronts share one block of 32
+// queries, wavefront t taking key tile t through the max, exponential and
+// probability work (the per-score VALU work, which bounds these short rows);
+// the exchanges keep the reference's order: every per-key partial sum is
+// e(tile 0) + e(tile 1), and wavefront 0 runs the one P.V MFMA chain over
+// both tiles, with wavefront 1's probabilities.
 template <int HD, int NW, bool CAUSAL, int MASK, bool POW2_SCALE, bool BLOCK_ORDER, int RES>
 __global__ void __launch_bounds__(NW * kWave)
 attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
@@ -105,8 +111,10 @@ attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
                      int ld_vt, int num_qblocks, float scale,
                      const int32_t* __restrict__ kv_len, const uint8_t* __restrict__ key_mask) {
   static_assert(HD == 8 || HD == 32 || HD == 64 || HD == 128 || HD == 256, "head_dim 8, 32, 64, 128 or 256");
+  constexpr bool kSplit = NW == 2 && RES == 2;
+  static_assert(NW != 2 || (RES == 2 && !BLOCK_ORDER), "two wavefronts: key split of two resident tiles");
   constexpr int kThreads = NW * kWave;
-  constexpr int kBQ = NW * 32;
+  constexpr int kBQ = kSplit ? 32 : NW * 32;
   constexpr int kTileElems = kBKV * HD;  // one K or V^T tile, bf16 elements
   constexpr int kChunksK = HD / 8;       // 16-byte chunks per K row
   // 16-deep MFMA steps of q.k.  Head dim 8 runs one step whose upper 8
@@ -126,6 +134,13 @@ attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
   bf16_t* sK = attn_lds;                        // buffer t at sK + t * kTileElems
   bf16_t* sV = attn_lds + kBufs * kTileElems;   // buffer t at sV + t * kTileElems
   uint8_t (*sM)[kBKV] = reinterpret_cast<uint8_t (*)[kBKV]>(attn_lds + 2 * kBufs * kTileElems);
+  // key split exchange areas (after the tiles, 16-byte aligned): the row max
+  // and min per wavefront and lane, then the weights e of each wavefront's
+  // tile ([wavefront][32 registers][64 lanes]), then wavefront 1's bf16
+  // probabilities ([64 lanes][4 fragments])
+  float* x_mm = reinterpret_cast<float*>(attn_lds) + (2 * kBufs * kTileElems * 2 + kBufs * kBKV + 15) / 16 * 4;
+  float* x_e = x_mm + 2 * 2 * kWave;
+  bf16x8* x_p = reinterpret_cast<bf16x8*>(x_e + 2 * 32 * kWave);
 
   // Block -> (batch*head, query tile).  Non-causal: MI355X hands consecutive
   // workgroups to its 8 XCDs round-robin; the id is remapped so each XCD walks
@@ -158,7 +173,7 @@ attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int l32 = lane & 31;
   const int lhi = lane >> 5;
-  const int qrow = q0 + wave * 32 + l32;  // the query this lane owns
+  const int qrow = q0 + (kSplit ? 0 : wave * 32) + l32;  // the query this lane owns
 
   int kv_limit = S;  // keys >= kv_limit are excluded
   if constexpr (MASK == kMaskPrefix) kv_limit = min(S, static_cast<int>(kv_len[b]));
@@ -167,7 +182,7 @@ attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
 
   if (MASK == kMaskPrefix && q0 >= kv_limit) {
     // Whole query tile is padding: zeros, no work.
-    if (qrow < S) {
+    if (qrow < S && (!kSplit || wave == 0)) {
       if constexpr (HD >= 16) {
 #pragma unroll
         for (int c = 0; c < HD / 16; ++c)
@@ -305,7 +320,7 @@ attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
     }
   };
 
-  const int wq_first = q0 + wave * 32;
+  const int wq_first = q0 + (kSplit ? 0 : wave * 32);
   const int wq_last = wq_first + 31;
   // tiles of the natural order this wavefront multiplies (causal: those with
   // a key <= its last query)
@@ -387,7 +402,7 @@ attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
   // the weights e of sweep B, and sweep C reuses those e (the same values it
   // would recompute), so every score's exponential is evaluated once.
   constexpr bool kCache = RES == 2;
-  f32x16 cache[kCache ? 2 : 1][2];
+  f32x16 cache[kCache && !kSplit ? 2 : 1][2];
   auto load_resident = [&]() {
     for (int t = 0; t < nkb; ++t) issue_tile(t, t, true);
     __builtin_amdgcn_s_waitcnt(kWaitVm0);
@@ -419,7 +434,10 @@ attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
       }
     }
   };
-  if constexpr (kCache) {
+  if constexpr (kSplit) {
+    load_resident();
+    if (wave < active) max_body(wave, wave, cache[0]);
+  } else if constexpr (kCache) {
     load_resident();
 #pragma unroll
     for (int t = 0; t < 2; ++t)
@@ -431,6 +449,14 @@ attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
     });
   }
   mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+  if constexpr (kSplit) {
+    mn = fminf(mn, __shfl_xor(mn, 32, kWave));
+    x_mm[wave * kWave + lane] = mx;
+    x_mm[(2 + wave) * kWave + lane] = mn;
+    __syncthreads();
+    mx = fmaxf(x_mm[lane], x_mm[kWave + lane]);
+    mn = fminf(x_mm[2 * kWave + lane], x_mm[3 * kWave + lane]);
+  }
   auto to_score = [&](float raw) {
     const float rq = round_bf16(raw);
     return POW2_SCALE ? rq * scale : round_bf16(rq * scale);
@@ -458,7 +484,33 @@ attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
       part[0][r] = 0.f;
       part[1][r] = 0.f;
     }
-    if constexpr (kCache) {
+    if constexpr (kSplit) {
+      // this wavefront's weights, zeros for a tile no query of the block sees
+      if (wave < active) {
+        dots_to_gaps(wave, wave * kBKV, row_max, raw_max_bf, true, cache[0]);
+#pragma unroll
+        for (int kb32 = 0; kb32 < 2; ++kb32)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) cache[0][kb32][r] = expf_nonpos(cache[0][kb32][r]);
+      } else {
+#pragma unroll
+        for (int kb32 = 0; kb32 < 2; ++kb32)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) cache[0][kb32][r] = 0.f;
+      }
+#pragma unroll
+      for (int kb32 = 0; kb32 < 2; ++kb32)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) x_e[(wave * 32 + kb32 * 16 + r) * kWave + lane] = cache[0][kb32][r];
+      __syncthreads();
+      // partial = e(tile 0) + e(tile 1), the order of the one-wavefront loop
+      // (0 + e0 = e0 exactly, and an unseen tile adds +0)
+#pragma unroll
+      for (int kb32 = 0; kb32 < 2; ++kb32)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          part[kb32][r] = x_e[(kb32 * 16 + r) * kWave + lane] + x_e[(32 + kb32 * 16 + r) * kWave + lane];
+    } else if constexpr (kCache) {
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         if (t >= active) continue;
@@ -585,8 +637,7 @@ attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[db][r] = 0.f;
   // s holds the gaps, or (have_e) the weights e themselves
-  auto pv_body = [&](int buf, f32x16 (&s)[2], bool have_e) {
-    bf16x8 pf[4];
+  auto make_pf = [&](f32x16 (&s)[2], bool have_e, bf16x8 (&pf)[4]) {
     if (BLOCK_ORDER || !slow_div) {
 #pragma unroll
       for (int kb32 = 0; kb32 < 2; ++kb32) {
@@ -614,6 +665,8 @@ attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
         }
       }
     }
+  };
+  auto pv_mfma = [&](int buf, const bf16x8 (&pf)[4]) {
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
 #pragma unroll
@@ -624,7 +677,28 @@ attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
       }
     }
   };
-  if constexpr (kCache) {
+  auto pv_body = [&](int buf, f32x16 (&s)[2], bool have_e) {
+    bf16x8 pf[4];
+    make_pf(s, have_e, pf);
+    pv_mfma(buf, pf);
+  };
+  if constexpr (kSplit) {
+    bf16x8 pf[4];
+    if (wave < active) make_pf(cache[0], true, pf);
+    if (wave == 1 && active > 1) {
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) x_p[lane * 4 + kk] = pf[kk];
+    }
+    __syncthreads();
+    if (wave == 1) return;
+    if (active > 0) pv_mfma(0, pf);
+    if (active > 1) {
+      bf16x8 pf1[4];
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) pf1[kk] = x_p[lane * 4 + kk];
+      pv_mfma(1, pf1);
+    }
+  } else if constexpr (kCache) {
 #pragma unroll
     for (int t = 0; t < 2; ++t)
       if (t < active) pv_body(t, cache[t], true);
@@ -656,17 +730,21 @@ attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
   }
 }
 
-// LDS bytes of one attention workgroup: K and V^T tiles plus key-mask bytes
-constexpr size_t attn_lds_bytes(int hd, int res) {
-  return static_cast<size_t>(res > 0 ? res : 2) * (2 * kBKV * hd * sizeof(bf16_t) + kBKV);
+// LDS bytes of one attention workgroup: K and V^T tiles plus key-mask bytes,
+// and with the key split (two wavefronts) the exchange areas
+constexpr size_t attn_lds_bytes(int hd, int res, bool split = false) {
+  const size_t tiles = static_cast<size_t>(res > 0 ? res : 2) * (2 * kBKV * hd * sizeof(bf16_t) + kBKV);
+  if (!split) return tiles;
+  return (tiles + 15) / 16 * 16 + (2 * 2 * kWave + 2 * 32 * kWave) * sizeof(float) + kWave * 4 * 16;
 }
 
 template <int HD, int NW, bool CAUSAL, int MASK, bool POW2, bool BLOCK_ORDER, int RES = 0>
 hipError_t launch_attn(const bf16_t* q, const bf16_t* k, const bf16_t* vt, bf16_t* ctx, int B,
                        int H, int S, float scale, const int32_t* kv_len, const uint8_t* key_mask,
                        hipStream_t st) {
-  constexpr int kBQ = NW * 32;
-  constexpr size_t kLds = attn_lds_bytes(HD, RES);
+  constexpr bool kSplit = NW == 2 && RES == 2;
+  constexpr int kBQ = kSplit ? 32 : NW * 32;
+  constexpr size_t kLds = attn_lds_bytes(HD, RES, kSplit);
   const int nqb = (S + kBQ - 1) / kBQ;
   const dim3 grid(static_cast<uint32_t>(B) * H * nqb);
   const int ld_vt = static_cast<int>(vt_stride(S));
@@ -689,16 +767,18 @@ hipError_t dispatch_order(const bf16_t* q, const bf16_t* k, const bf16_t* vt, bf
                           const uint8_t* key_mask, hipStream_t st) {
   if (S > kWarpSoftmaxMaxKeys)
     return launch_attn<HD, 4, CAUSAL, MASK, POW2, true>(q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
-  // Small problems use one-wavefront workgroups (32 queries) so more of the
-  // 256 CUs get work; larger ones share each K/V tile among 4 wavefronts.
+  // Small problems use workgroups of 32 queries (one wavefront, or two that
+  // split the keys) so more of the 256 CUs get work; larger ones share each
+  // K/V tile among 4 wavefronts.
   // Rows of at most 256 keys keep every tile resident in LDS (at most 128 keys
   // for head dim 256, whose four resident tiles would exceed the 160 KiB of
   // LDS of a CU).
   constexpr bool kRes4 = attn_lds_bytes(HD, 4) <= 160 * 1024;
   const int64_t groups128 = static_cast<int64_t>(B) * H * ((S + 127) / 128);
   if (groups128 < 512) {
+    // rows of at most 128 keys: two wavefronts per 32 queries (key split)
     if (S <= 2 * kBKV)
-      return launch_attn<HD, 1, CAUSAL, MASK, POW2, false, 2>(q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
+      return launch_attn<HD, 2, CAUSAL, MASK, POW2, false, 2>(q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
     if constexpr (kRes4) {
       if (S <= 4 * kBKV)
         return launch_attn<HD, 1, CAUSAL, MASK, POW2, false, 4>(q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
