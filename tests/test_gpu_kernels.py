@@ -182,12 +182,14 @@ def test_linear_residual(device, m, n, k, epi):
 
 @pytest.mark.parametrize(
     "m,n,k",
-    [(8192, 96, 32), (8192, 32, 32), (37, 96, 32), (1, 32, 32), (300, 64, 96), (8192, 384, 128), (8192, 128, 128)],
+    [(8192, 96, 32), (8192, 32, 32), (37, 96, 32), (1, 32, 32), (300, 64, 96), (8192, 384, 128), (8192, 128, 128),
+     (128, 384, 128), (37, 128, 128), (256, 128, 384), (1, 384, 128)],
 )
 def test_linear_narrow_and_d128_shapes_bitwise(device, m, n, k):
     """The official matrix's projection shapes: d_model 32 (N or K not a
-    multiple of 64: the one-block-per-wavefront kernel) and d_model 128; every
-    epilogue equals torch's bf16 ops bit for bit."""
+    multiple of 64: the one-block-per-wavefront kernel) and d_model 128 (with
+    up to 256 rows: the skinny kernel's 128-wide K stages); every epilogue
+    equals torch's bf16 ops bit for bit."""
     a, w, bias, res, _ = _linear_case(device, m, n, k, 29 * m + n + k)
     ref = F.linear(a, w, bias)
     assert torch.equal(native.linear(a, w, bias, native.ENC_EPI_BIAS), ref)

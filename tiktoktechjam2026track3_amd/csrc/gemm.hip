@@ -710,8 +710,9 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
 //   A operand : row l%16, k = 4*(l/16) + j      (j = 0..3, 8 contiguous bytes)
 //   B operand : col l%16, k = 4*(l/16) + j      (a W row, 8 contiguous bytes)
 //   C/D       : col l%16, row = 4*(l/16) + j
-// A and W stream through a two-stage LDS ring in K slices of 256 (512 bytes a
-// row) with direct global->LDS loads: one instruction moves two whole rows, so
+// A and W stream through a two-stage LDS ring in K slices of KS = 256 (512
+// bytes a row; KS = 128 when K is a multiple of 128 only, e.g. d_model 128)
+// with direct global->LDS loads: one instruction moves 1 KiB of whole rows, so
 // global reads are fully coalesced.  Inside a row the 16-byte chunk c sits in
 // slot c ^ (row & 15), so the 16 rows one fragment read touches fall in
 // distinct bank groups.
@@ -722,8 +723,6 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
 //               ... (the library's split order); the partials meet in LDS and
 //               are added in order before the bias.
 constexpr int kSkinnyMaxRows = 256;  // products with at most this many rows use it
-constexpr int kSkinnyKS = 256;       // K elements per LDS stage
-constexpr int kSkinnyRow = kSkinnyKS;  // LDS row length, elements
 
 template <int EPI>
 __device__ __forceinline__ void store_one(const GemmEpilogueArgs& ep, int N, int row, int col, float acc,
@@ -749,18 +748,21 @@ __device__ __forceinline__ void store_one(const GemmEpilogueArgs& ep, int N, int
   }
 }
 
-template <int EPI, int SPLIT, int CW>
+template <int EPI, int SPLIT, int CW, int KS>
 __global__ void __launch_bounds__(256)
 gemm_skinny_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int M, int N, int K,
                    GemmEpilogueArgs ep) {
   constexpr int kWaves = SPLIT == 1 ? 4 : SPLIT;
   constexpr int kBN = SPLIT == 1 ? 64 : 16;
   constexpr int kRows = 16 + kBN;                       // LDS rows per stage (A then W)
-  constexpr int kStage = kRows * kSkinnyRow;            // elements per stage
-  constexpr int kLoads = kRows / 2 / kWaves;            // 2-row load instructions per wavefront
+  constexpr int kStage = kRows * KS;                    // elements per stage
+  constexpr int kChunksRow = KS / 8;                    // 16-byte chunks per LDS row
+  constexpr int kRowsPerLoad = kWave / kChunksRow;      // rows one load instruction fills
+  constexpr int kLoads = kRows / kRowsPerLoad / kWaves;  // load instructions per wavefront
   constexpr int kStepsPerChunk = CW / 16;
-  static_assert(kRows % (2 * kWaves) == 0, "load split");
-  static_assert(SPLIT == 1 || (CW % 16 == 0 && kSkinnyKS % (CW * SPLIT) == 0), "chunk width");
+  static_assert(KS == 128 || KS == 256, "stage width");
+  static_assert(kRows % (kRowsPerLoad * kWaves) == 0, "load split");
+  static_assert(SPLIT == 1 || (CW % 16 == 0 && KS % (CW * SPLIT) == 0), "chunk width");
   __shared__ __attribute__((aligned(16))) bf16_t smem[2 * kStage];
   __shared__ float red[SPLIT > 1 ? SPLIT : 1][64][4];
 
@@ -783,30 +785,31 @@ gemm_skinny_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, i
   const int l16 = lane & 15;
   const int g = lane >> 4;
 
-  // Load instruction j of wavefront w fills LDS rows 2(kWaves j + w) and +1;
-  // lane L writes slot L%32 of row +L/32, holding chunk (L%32) ^ (row & 15).
-  const int ld_half = lane >> 5;
+  // Load instruction j of wavefront w fills LDS rows R (kWaves j + w) .. +R-1
+  // (R = rows per instruction); lane L writes slot L % C of row + L / C (C =
+  // chunks per row), holding chunk (L % C) ^ (row & 15).
+  const int ld_row = lane / kChunksRow;
   auto issue_stage = [&](int stage, int k0) {
     bf16_t* base = smem + stage * kStage;
 #pragma unroll
     for (int j = 0; j < kLoads; ++j) {
-      const int r0 = 2 * (kWaves * j + wave);
-      const int r = r0 + ld_half;
-      const int chunk = (lane & 31) ^ (r & 15);
+      const int r0 = kRowsPerLoad * (kWaves * j + wave);
+      const int r = r0 + ld_row;
+      const int chunk = (lane % kChunksRow) ^ (r & 15);
       const bf16_t* src;
       if (r < 16) {
         src = A + static_cast<int64_t>(min(m0 + r, M - 1)) * K;  // rows past M: a valid row, never stored
       } else {
         src = W + static_cast<int64_t>(n0 + r - 16) * K;
       }
-      __builtin_amdgcn_global_load_lds(src + k0 + chunk * 8, base + r0 * kSkinnyRow, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(src + k0 + chunk * 8, base + r0 * KS, 16, 0, 0);
     }
   };
   // fragment (8 bytes) of LDS row r at K-step s of the stage: chunk 2s + g/2
   auto frag = [&](int stage, int r, int s) {
     typedef short s16x4 __attribute__((ext_vector_type(4)));
     const int chunk = 2 * s + (g >> 1);
-    const bf16_t* p = smem + stage * kStage + r * kSkinnyRow + ((chunk ^ (r & 15)) << 3) + 4 * (g & 1);
+    const bf16_t* p = smem + stage * kStage + r * KS + ((chunk ^ (r & 15)) << 3) + 4 * (g & 1);
     return *reinterpret_cast<const s16x4*>(p);
   };
 
@@ -840,9 +843,9 @@ gemm_skinny_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, i
     }
   }
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  const int nst = K / kSkinnyKS;
+  const int nst = K / KS;
   issue_stage(0, 0);
-  if (nst > 1) issue_stage(1, kSkinnyKS);
+  if (nst > 1) issue_stage(1, KS);
   for (int st = 0; st < nst; ++st) {
     const int buf = st & 1;
     // the other stage's loads may still be in flight
@@ -853,14 +856,14 @@ gemm_skinny_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, i
     }
     ring_barrier();
 #pragma unroll
-    for (int s = 0; s < kSkinnyKS / 16; ++s) {
+    for (int s = 0; s < KS / 16; ++s) {
       bool mine = true;
       if constexpr (SPLIT > 1) mine = ((s / kStepsPerChunk) % SPLIT) == wave;
       if (mine) acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(frag(buf, l16, s), frag(buf, wrow, s), acc, 0, 0, 0);
     }
     __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 0));
     ring_barrier();  // every wavefront is done reading this stage
-    if (st + 2 < nst) issue_stage(buf, (st + 2) * kSkinnyKS);
+    if (st + 2 < nst) issue_stage(buf, (st + 2) * KS);
   }
 
   if constexpr (SPLIT > 1) {
@@ -894,18 +897,18 @@ gemm_skinny_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, i
   }
 }
 
-template <int SPLIT, int CW>
+template <int SPLIT, int CW, int KS>
 hipError_t launch_skinny(const bf16_t* A, const bf16_t* W, int M, int N, int K, int epi,
                          const GemmEpilogueArgs& ep, hipStream_t st) {
   constexpr int kWaves = SPLIT == 1 ? 4 : SPLIT;
   constexpr int kBN = SPLIT == 1 ? 64 : 16;
   const dim3 grid(((M + 15) / 16) * (N / kBN)), block(kWaves * kWave);
   switch (epi) {
-    case kEpiBias: hipLaunchKernelGGL((gemm_skinny_kernel<kEpiBias, SPLIT, CW>), grid, block, 0, st, A, W, M, N, K, ep); break;
-    case kEpiBiasGelu: hipLaunchKernelGGL((gemm_skinny_kernel<kEpiBiasGelu, SPLIT, CW>), grid, block, 0, st, A, W, M, N, K, ep); break;
-    case kEpiResidualKeep: hipLaunchKernelGGL((gemm_skinny_kernel<kEpiResidualKeep, SPLIT, CW>), grid, block, 0, st, A, W, M, N, K, ep); break;
-    case kEpiResidualZero: hipLaunchKernelGGL((gemm_skinny_kernel<kEpiResidualZero, SPLIT, CW>), grid, block, 0, st, A, W, M, N, K, ep); break;
-    case kEpiQkvHeadMajor: hipLaunchKernelGGL((gemm_skinny_kernel<kEpiQkvHeadMajor, SPLIT, CW>), grid, block, 0, st, A, W, M, N, K, ep); break;
+    case kEpiBias: hipLaunchKernelGGL((gemm_skinny_kernel<kEpiBias, SPLIT, CW, KS>), grid, block, 0, st, A, W, M, N, K, ep); break;
+    case kEpiBiasGelu: hipLaunchKernelGGL((gemm_skinny_kernel<kEpiBiasGelu, SPLIT, CW, KS>), grid, block, 0, st, A, W, M, N, K, ep); break;
+    case kEpiResidualKeep: hipLaunchKernelGGL((gemm_skinny_kernel<kEpiResidualKeep, SPLIT, CW, KS>), grid, block, 0, st, A, W, M, N, K, ep); break;
+    case kEpiResidualZero: hipLaunchKernelGGL((gemm_skinny_kernel<kEpiResidualZero, SPLIT, CW, KS>), grid, block, 0, st, A, W, M, N, K, ep); break;
+    case kEpiQkvHeadMajor: hipLaunchKernelGGL((gemm_skinny_kernel<kEpiQkvHeadMajor, SPLIT, CW, KS>), grid, block, 0, st, A, W, M, N, K, ep); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -1014,9 +1017,11 @@ int pick_big_tile(int64_t M, int64_t N, const bf16_t* A, const bf16_t* W, const 
   auto al = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
   if (!al(A) || !al(W) || !al(ep.out) || !al(ep.residual) || !al(ep.q) || !al(ep.k) || !al(ep.v_t)) return 0;
   if (M < 1024) return 0;
+  const int64_t t256x128 = ((M + 255) / 256) * (N / 128);
   // The erf GELU epilogue is long dependent VALU work; with two resident
-  // 256x128 tiles per CU one tile's epilogue overlaps the other's MFMA loop.
-  if (ep_is_gelu && N % 128 == 0) return 256129;
+  // 256x128 tiles per CU one tile's epilogue overlaps the other's MFMA loop
+  // (when there are tiles for two per CU: a narrow N leaves most CUs idle).
+  if (ep_is_gelu && N % 128 == 0 && t256x128 >= 2 * num_cus) return 256129;
   // Whole rounds of tiles over the CUs times the tile's work, over its
   // measured per-tile efficiency (256x128 tiles run ~10% below 256x256).
   auto cost = [&](int bm, int bn, double eff) {
@@ -1024,7 +1029,6 @@ int pick_big_tile(int64_t M, int64_t N, const bf16_t* A, const bf16_t* W, const 
     const int64_t rounds = (tiles + num_cus - 1) / num_cus;
     return static_cast<double>(rounds) * bm * bn / eff;
   };
-  const int64_t t256x128 = ((M + 255) / 256) * (N / 128);
   if (N % 256 == 0 && cost(256, 256, 1.0) <= cost(256, 128, 0.9)) return 256256;
   if (N % 128 == 0 && t256x128 >= num_cus) return 256128;
   if (N % 128 == 0) return 128128;
@@ -1097,13 +1101,21 @@ hipError_t gemm_bf16(const bf16_t* A, const bf16_t* W, int64_t M, int64_t N, int
   gemm_split_plan(M, N, K, &split, &chunk);
   const bool aligned16 = reinterpret_cast<uintptr_t>(A) % 16 == 0 && reinterpret_cast<uintptr_t>(W) % 16 == 0;
   // whole LDS stages, each holding whole rounds of the split's chunks
-  const bool whole = K % kSkinnyKS == 0 && kSkinnyKS % (chunk * split) == 0;
-  if (M <= kSkinnyMaxRows && aligned16 && whole) {
-    if (split == 1) return launch_skinny<1, 16>(A, W, m, n, k, epi, ep, stream);
-    if (split == 4 && chunk == 32) return launch_skinny<4, 32>(A, W, m, n, k, epi, ep, stream);
-    if (split == 4 && chunk == 64) return launch_skinny<4, 64>(A, W, m, n, k, epi, ep, stream);
-    if (split == 2 && chunk == 128) return launch_skinny<2, 128>(A, W, m, n, k, epi, ep, stream);
+  const bool whole = K % 256 == 0 && 256 % (chunk * split) == 0;
+  // With K <= 256 (d_model 128 or 256) a product stays latency-bound well past
+  // 256 rows, and the 16-row tiles put the most workgroups in flight: up to
+  // 2048 rows, and up to 8192 rows for N <= 128 (measured on MI355X against
+  // the large tiles and the 64x64 tiles).
+  const bool skinny_rows = M <= kSkinnyMaxRows || (K <= 256 && (M <= 2048 || (N <= 128 && M <= 8192)));
+  if (skinny_rows && aligned16 && whole) {
+    if (split == 1) return launch_skinny<1, 16, 256>(A, W, m, n, k, epi, ep, stream);
+    if (split == 4 && chunk == 32) return launch_skinny<4, 32, 256>(A, W, m, n, k, epi, ep, stream);
+    if (split == 4 && chunk == 64) return launch_skinny<4, 64, 256>(A, W, m, n, k, epi, ep, stream);
+    if (split == 2 && chunk == 128) return launch_skinny<2, 128, 256>(A, W, m, n, k, epi, ep, stream);
   }
+  // K a multiple of 128 only (d_model 128): 128-wide stages, sequential K
+  if (skinny_rows && aligned16 && split == 1 && K % 128 == 0)
+    return launch_skinny<1, 16, 128>(A, W, m, n, k, epi, ep, stream);
   if (split == 4 && chunk == 32) return launch_split<4, 32>(A, W, m, n, k, epi, ep, stream);
   if (split == 4 && chunk == 64) return launch_split<4, 64>(A, W, m, n, k, epi, ep, stream);
   if (split == 2 && chunk == 128) return launch_split<2, 128>(A, W, m, n, k, epi, ep, stream);
