@@ -151,12 +151,81 @@ layernorm_kernel(const bf16_t* __restrict__ x, const bf16_t* __restrict__ gamma,
   }
 }
 
+// Rows narrower than 256 (L = WIDTH / 4 < 64 vectors): 64 / L rows share a
+// wavefront, L lanes (one vector each) per row.  The reference reduces such a
+// row on a 64-lane warp whose lanes >= L hold empty (count 0) states, and
+// merging an empty state is not an identity (the merge weights come from the
+// hardware reciprocal of the count), so those merges are reproduced: at
+// shuffle offsets >= L every lane merges an empty state, and below L a lane
+// whose partner lies past its row's L lanes merges an empty state instead of
+// the shuffled one (lane 0 of a row never reads another row's lanes).  The
+// other virtual warps are empty: their merges follow as (w0 <- E) <- (E <- E).
+template <int WIDTH>
+__global__ void __launch_bounds__(kRowsPerBlock * kWave)
+layernorm_packed_kernel(const bf16_t* __restrict__ x, const bf16_t* __restrict__ gamma,
+                        const bf16_t* __restrict__ beta, bf16_t* __restrict__ y, int64_t rows, float eps,
+                        const uint8_t* __restrict__ row_mask) {
+  constexpr int L = WIDTH / 4;   // lanes per row
+  constexpr int R = kWave / L;   // rows per wavefront
+  static_assert(L >= 8 && L <= 32, "packed widths 32..128");
+  const int lane = threadIdx.x % kWave;
+  const int seg = lane / L;      // this lane's row within the wavefront
+  const int j = lane % L;        // this lane's vector within the row
+  const int64_t row = (static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + threadIdx.x / kWave) * R + seg;
+  const bool live = row < rows;  // every lane stays for the shuffles
+  const int64_t base = (live ? row : 0) * WIDTH + j * 4;
+
+  const u32x2 w = *reinterpret_cast<const u32x2*>(x + base);
+  const u32x2 gw = *reinterpret_cast<const u32x2*>(gamma + j * 4);
+  const u32x2 bw = *reinterpret_cast<const u32x2*>(beta + j * 4);
+  const float v[4] = {lo_bf16(w[0]), hi_bf16(w[0]), lo_bf16(w[1]), hi_bf16(w[1])};
+
+  Welford st = {0.f, 0.f, 0.f};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) st = welford_add(st, v[e]);
+  const Welford empty = {0.f, 0.f, 0.f};
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    if (off >= L) {
+      st = welford_merge(st, empty);
+    } else {
+      Welford p = shfl_down(st, off);
+      if (j + off >= L) p = empty;
+      st = welford_merge(st, p);
+    }
+  }
+  st = welford_merge(welford_merge(st, empty), welford_merge(empty, empty));
+  const float mean = __shfl(st.mean, seg * L, kWave);
+  const float var = __shfl(st.m2, seg * L, kWave) / static_cast<float>(WIDTH);
+  const float rstd = rsqrtf(var + eps);
+  if (!live) return;
+
+  u32x2 out = {0u, 0u};
+  if (row_mask == nullptr || row_mask[row] != 0) {
+    const float g[4] = {lo_bf16(gw[0]), hi_bf16(gw[0]), lo_bf16(gw[1]), hi_bf16(gw[1])};
+    const float b[4] = {lo_bf16(bw[0]), hi_bf16(bw[0]), lo_bf16(bw[1]), hi_bf16(bw[1])};
+    float o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = fmaf(g[e], rstd * (v[e] - mean), b[e]);
+    out = u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+  }
+  *reinterpret_cast<u32x2*>(y + base) = out;
+}
+
 template <int WIDTH>
 hipError_t launch_ln(const bf16_t* x, const bf16_t* g, const bf16_t* b, bf16_t* y,
                      int64_t rows, float eps, const uint8_t* mask, hipStream_t st) {
-  const int64_t blocks = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
-  hipLaunchKernelGGL(layernorm_kernel<WIDTH>, dim3(static_cast<uint32_t>(blocks)),
-                     dim3(kRowsPerBlock * kWave), 0, st, x, g, b, y, rows, eps, mask);
+  if constexpr (WIDTH < 256) {
+    constexpr int kRowsPerWave = kWave / (WIDTH / 4);
+    const int64_t per_block = static_cast<int64_t>(kRowsPerBlock) * kRowsPerWave;
+    const int64_t blocks = (rows + per_block - 1) / per_block;
+    hipLaunchKernelGGL(layernorm_packed_kernel<WIDTH>, dim3(static_cast<uint32_t>(blocks)),
+                       dim3(kRowsPerBlock * kWave), 0, st, x, g, b, y, rows, eps, mask);
+  } else {
+    const int64_t blocks = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
+    hipLaunchKernelGGL(layernorm_kernel<WIDTH>, dim3(static_cast<uint32_t>(blocks)),
+                       dim3(kRowsPerBlock * kWave), 0, st, x, g, b, y, rows, eps, mask);
+  }
   return hipGetLastError();
 }
 
