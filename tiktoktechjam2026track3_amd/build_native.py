@@ -32,6 +32,7 @@ SOURCES = (
     "attention_hd128.hip",
     "attention_hd256.hip",
     "flash_attention.hip",
+    "block_tail.hip",
     "capi.hip",
 )
 

@@ -287,6 +287,15 @@ int enc_encoder_forward_bf16(const void* x, void* out, void* workspace, int64_t 
   const float scale = 1.0f / sqrtf(static_cast<float>(D / H));
   auto W = [&](int64_t layer, int idx) { return static_cast<const bf16_t*>(weights[layer * 12 + idx]); };
 
+  // Narrow models with up to 8192 tokens run the block tail (out_proj ..
+  // ffn_out) as one kernel, whose 16-byte loads need 16-byte aligned weights.
+  // (With more tokens the four launches win: the fused kernel's one workgroup
+  // per CU cannot hide its per-slab latency; measured on MI355X.)
+  bool tail_fused = enc::block_tail_supported(D, F) && T <= 8192;
+  for (int64_t layer = 0; tail_fused && layer < num_layers; ++layer)
+    for (int idx = 4; idx < 12; ++idx)
+      tail_fused = tail_fused && reinterpret_cast<uintptr_t>(W(layer, idx)) % 16 == 0;
+
   const bf16_t* cur = static_cast<const bf16_t*>(x);
   hipError_t e = hipSuccess;
   for (int64_t layer = 0; layer < num_layers; ++layer) {
@@ -312,6 +321,26 @@ int enc_encoder_forward_bf16(const void* x, void* out, void* workspace, int64_t 
     e = attention(q, k, vt, ctx, static_cast<int>(batch), static_cast<int>(H), static_cast<int>(seq_len),
                   static_cast<int>(D / H), scale, causal != 0, kv_len, key_mask, st);
     if (e != hipSuccess) return fail_hip(e, "encoder attention");
+    if (tail_fused) {
+      // out_proj .. ffn_out in one launch (narrow models), same arithmetic
+      enc::BlockTailArgs ta;
+      ta.ctx = ctx;
+      ta.x = cur;
+      ta.wo = W(layer, 4);
+      ta.bo = W(layer, 5);
+      ta.g2 = W(layer, 6);
+      ta.be2 = W(layer, 7);
+      ta.w1 = W(layer, 8);
+      ta.b1 = W(layer, 9);
+      ta.w2 = W(layer, 10);
+      ta.b2 = W(layer, 11);
+      ta.out = x_attn;
+      ta.row_mask = row_mask;
+      e = enc::block_tail_bf16(ta, T, D, F, eps, cus, st);
+      if (e != hipSuccess) return fail_hip(e, "encoder block tail");
+      cur = x_attn;
+      continue;
+    }
     // out_proj + residual; padded rows keep the residual (attention output is 0 there)
     enc::GemmEpilogueArgs oa;
     oa.bias = W(layer, 5);

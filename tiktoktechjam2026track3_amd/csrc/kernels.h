@@ -82,6 +82,27 @@ hipError_t flash_attention_fwd_bf16(const bf16_t* q, const bf16_t* k, const bf16
                                     bool causal, const int32_t* kv_len, const uint8_t* key_mask,
                                     hipStream_t stream);
 
+// Fused block tail for d_model and ffn_dim of 32, 64 or 128: out_proj +
+// residual (rows masked out keep x), norm2, ffn_in + GELU, ffn_out + residual
+// (rows masked out become 0), bitwise the same as the four separate launches.
+struct BlockTailArgs {
+  const bf16_t* ctx = nullptr;  // attention context [T, D]
+  const bf16_t* x = nullptr;    // block input (residual) [T, D]
+  const bf16_t* wo = nullptr;   // out_proj weight [D, D] and bias [D]
+  const bf16_t* bo = nullptr;
+  const bf16_t* g2 = nullptr;   // norm2 weight and bias [D]
+  const bf16_t* be2 = nullptr;
+  const bf16_t* w1 = nullptr;   // ffn_in weight [F, D] and bias [F]
+  const bf16_t* b1 = nullptr;
+  const bf16_t* w2 = nullptr;   // ffn_out weight [D, F] and bias [D]
+  const bf16_t* b2 = nullptr;
+  bf16_t* out = nullptr;        // block output [T, D]; may alias x
+  const uint8_t* row_mask = nullptr;
+};
+bool block_tail_supported(int64_t d_model, int64_t ffn_dim);
+hipError_t block_tail_bf16(const BlockTailArgs& args, int64_t rows, int64_t d_model, int64_t ffn_dim, float eps,
+                           int num_cus, hipStream_t stream);
+
 // Sequence lengths whose softmax summation order is reproduced exactly.
 bool attention_seq_supported(int64_t seq_len);
 

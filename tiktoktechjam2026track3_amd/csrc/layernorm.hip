@@ -23,51 +23,13 @@
 // the merge order all agree bit for bit.
 #include "common.h"
 #include "kernels.h"
+#include "welford.h"
 
 namespace enc {
 
 namespace {
 
 constexpr int kRowsPerBlock = 4;  // one row per wavefront, 4 wavefronts
-
-struct Welford {
-  float mean, m2, count;
-};
-
-// v_rcp_f32 of a value the compiler may know; the asm keeps it from folding.
-__device__ __forceinline__ float hw_rcp(float n) {
-  float r;
-  asm("v_rcp_f32 %0, %1" : "=v"(r) : "v"(n));
-  return r;
-}
-
-__device__ __forceinline__ Welford welford_add(Welford s, float x) {
-#pragma clang fp contract(off)
-  const float delta = x - s.mean;
-  const float n = s.count + 1.f;
-  const float mean = fmaf(delta, hw_rcp(n), s.mean);
-  const float m2 = s.m2 + delta * (x - mean);
-  return {mean, m2, n};
-}
-
-// combine(b = running, a = incoming), the operand roles of the native merge.
-__device__ __forceinline__ Welford welford_merge(Welford b, Welford a) {
-#pragma clang fp contract(off)
-  const float delta = b.mean - a.mean;
-  const float n = a.count + b.count;
-  if (!(n > 0.f)) return {0.f, 0.f, n};
-  const float coef = hw_rcp(n);
-  const float na = a.count * coef;
-  const float nb = b.count * coef;
-  const float mean = na * a.mean + nb * b.mean;
-  const float m2 = fmaf(delta * delta * a.count, nb, a.m2 + b.m2);
-  return {mean, m2, n};
-}
-
-__device__ __forceinline__ Welford shfl_down(Welford s, int off) {
-  return {__shfl_down(s.mean, off, kWave), __shfl_down(s.m2, off, kWave),
-          __shfl_down(s.count, off, kWave)};
-}
 
 // WIDTH = row width; the row is WIDTH/4 vectors, lane l holds vectors
 // l + 64 s (s < SLOTS).  Narrow rows (WIDTH < 256) leave lanes and whole
@@ -152,14 +114,8 @@ layernorm_kernel(const bf16_t* __restrict__ x, const bf16_t* __restrict__ gamma,
 }
 
 // Rows narrower than 256 (L = WIDTH / 4 < 64 vectors): 64 / L rows share a
-// wavefront, L lanes (one vector each) per row.  The reference reduces such a
-// row on a 64-lane warp whose lanes >= L hold empty (count 0) states, and
-// merging an empty state is not an identity (the merge weights come from the
-// hardware reciprocal of the count), so those merges are reproduced: at
-// shuffle offsets >= L every lane merges an empty state, and below L a lane
-// whose partner lies past its row's L lanes merges an empty state instead of
-// the shuffled one (lane 0 of a row never reads another row's lanes).  The
-// other virtual warps are empty: their merges follow as (w0 <- E) <- (E <- E).
+// wavefront, L lanes (one vector each) per row; packed_row_stats reproduces
+// the reference's merges with the empty lanes of its 64-lane warp.
 template <int WIDTH>
 __global__ void __launch_bounds__(kRowsPerBlock * kWave)
 layernorm_packed_kernel(const bf16_t* __restrict__ x, const bf16_t* __restrict__ gamma,
@@ -180,24 +136,8 @@ layernorm_packed_kernel(const bf16_t* __restrict__ x, const bf16_t* __restrict__
   const u32x2 bw = *reinterpret_cast<const u32x2*>(beta + j * 4);
   const float v[4] = {lo_bf16(w[0]), hi_bf16(w[0]), lo_bf16(w[1]), hi_bf16(w[1])};
 
-  Welford st = {0.f, 0.f, 0.f};
-#pragma unroll
-  for (int e = 0; e < 4; ++e) st = welford_add(st, v[e]);
-  const Welford empty = {0.f, 0.f, 0.f};
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    if (off >= L) {
-      st = welford_merge(st, empty);
-    } else {
-      Welford p = shfl_down(st, off);
-      if (j + off >= L) p = empty;
-      st = welford_merge(st, p);
-    }
-  }
-  st = welford_merge(welford_merge(st, empty), welford_merge(empty, empty));
-  const float mean = __shfl(st.mean, seg * L, kWave);
-  const float var = __shfl(st.m2, seg * L, kWave) / static_cast<float>(WIDTH);
-  const float rstd = rsqrtf(var + eps);
+  float mean, rstd;
+  packed_row_stats<L>(v, j, seg, eps, &mean, &rstd);
   if (!live) return;
 
   u32x2 out = {0u, 0u};
