@@ -88,23 +88,26 @@ def test_encoder_parity_official_cases(device, case_id):
 @pytest.mark.parametrize(
     "cfg",
     [TransformerConfig(3, 37, 128, 4, 64, 2, True), TransformerConfig(2, 45, 64, 2, 128, 2, False),
-     TransformerConfig(5, 19, 32, 1, 32, 3, True)],
-    ids=["d128-f64-causal", "d64-f128", "d32-f32-causal"],
+     TransformerConfig(2, 48, 64, 2, 128, 1, False), TransformerConfig(5, 19, 32, 1, 32, 3, True)],
+    ids=["d128-f64-causal", "d64-f128", "d64-f128-whole-slabs", "d32-f32-causal"],
 )
 def test_encoder_parity_narrow_ragged(device, cfg):
     """Narrow models run the fused block tail (out_proj .. ffn_out in one
     kernel): token counts that leave a partial 16-row slab, d_model != ffn_dim,
-    with and without padding, against the oracle bit for bit."""
+    with and without padding, against the oracle bit for bit, on the capturing
+    call and on two graph replays (a result read before its MFMA landed once
+    showed up only on some calls)."""
     sd, candidate = build_models(cfg, 77, device)
     for padding in (0.0, 0.3):
         with torch.inference_mode():
             x, mask = generate_random_case(cfg, device, torch.bfloat16, 5, padding, 1.0)
-            out = candidate(x, mask)
+            outs = [candidate(x, mask) for _ in range(3)]
             ref = encoder_forward(sd, x, mask, cfg.causal, cfg.num_heads, cfg.num_layers)
             torch.cuda.synchronize()
-        result = compare(ref, out, RTOL, ATOL)
+        result = compare(ref, outs[0], RTOL, ATOL)
         assert result["passed"], result
-        assert torch.equal(ref, out)
+        for out in outs:
+            assert torch.equal(ref, out)
 
 
 def test_encoder_parity_second_trial_c4(device):

@@ -52,16 +52,31 @@ __device__ __forceinline__ s16x4 tail_frag(const bf16_t* base, int row, int k0, 
   return *reinterpret_cast<const s16x4*>(base + row * tail_ld(K) + k0 + 4 * g);
 }
 
-// rows x K bf16 row-major (global) -> LDS with the padded stride
-template <int K>
-__device__ __forceinline__ void tail_load_rows(bf16_t* dst, const bf16_t* src, int nrows, int tid) {
-  constexpr int kChunks = K / 8;
-  for (int c = tid; c < nrows * kChunks; c += kTailThreads) {
-    const int r = c / kChunks, ch = c % kChunks;
-    *reinterpret_cast<u32x4*>(dst + r * tail_ld(K) + ch * 8) =
-        *reinterpret_cast<const u32x4*>(src + static_cast<int64_t>(r) * K + ch * 8);
+// NROWS x K bf16 row-major (global) <-> registers <-> LDS (padded stride):
+// chunk i of this thread is 16-byte chunk tid + 256 i of the matrix.  The
+// three weight matrices are loaded into registers together and only then
+// stored, so their loads share one memory round trip.
+template <int K, int NROWS>
+struct TailRows {
+  static constexpr int kChunks = K / 8;
+  static constexpr int kTotal = NROWS * kChunks;
+  static constexpr int kPer = (kTotal + kTailThreads - 1) / kTailThreads;  // chunks per thread
+  __device__ static void load(u32x4 (&v)[kPer], const bf16_t* src, int tid) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int c = min(tid + i * kTailThreads, kTotal - 1);
+      v[i] = *reinterpret_cast<const u32x4*>(src + static_cast<int64_t>(c / kChunks) * K + (c % kChunks) * 8);
+    }
   }
-}
+  __device__ static void store(const u32x4 (&v)[kPer], bf16_t* dst, int tid) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int c = tid + i * kTailThreads;
+      if (kTotal % kTailThreads == 0 || c < kTotal)
+        *reinterpret_cast<u32x4*>(dst + (c / kChunks) * tail_ld(K) + (c % kChunks) * 8) = v[i];
+    }
+  }
+};
 
 template <int D, int F>
 __global__ void __launch_bounds__(kTailThreads)
@@ -88,9 +103,18 @@ block_tail_kernel(const bf16_t* __restrict__ ctx, const bf16_t* __restrict__ x, 
   const int l16 = lane & 15;
   const int g = lane >> 4;
 
-  tail_load_rows<D>(sWo, wo, D, tid);
-  tail_load_rows<D>(sW1, w1, F, tid);
-  tail_load_rows<F>(sW2, w2, D, tid);
+  {
+    using RWo = TailRows<D, D>;
+    using RW1 = TailRows<D, F>;
+    using RW2 = TailRows<F, D>;
+    u32x4 vo[RWo::kPer], v1[RW1::kPer], v2[RW2::kPer];
+    RWo::load(vo, wo, tid);
+    RW1::load(v1, w1, tid);
+    RW2::load(v2, w2, tid);
+    RWo::store(vo, sWo, tid);
+    RW1::store(v1, sW1, tid);
+    RW2::store(v2, sW2, tid);
+  }
 
   // norm2's gamma / beta for this lane's vector (rows of D = 4 L elements)
   constexpr int L = D / 4;
@@ -123,6 +147,17 @@ block_tail_kernel(const bf16_t* __restrict__ ctx, const bf16_t* __restrict__ x, 
       *reinterpret_cast<u32x4*>(sX + my_r * kLdD + my_ch * 8) = next_x;
     }
     fetch(slab + gridDim.x);
+    // Row-mask verdicts of this lane's output rows 4g .. 4g+3, taken before
+    // the products: with no branch between an MFMA and the reads of its
+    // result, the compiler's wait states before those reads stay in place
+    // (a mask test between them left a result register read two
+    // instructions after its MFMA, before the write landed).
+    bool keep[4];
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int r = r0 + 4 * g + jj;
+      keep[jj] = row_mask == nullptr || (r < rows && row_mask[r] != 0);
+    }
     __syncthreads();
 
     // ---- out_proj + residual (rows masked out keep the residual) -> sX ----
@@ -137,10 +172,10 @@ block_tail_kernel(const bf16_t* __restrict__ ctx, const bf16_t* __restrict__ x, 
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
         const int r = 4 * g + jj;
-        const bool keep = row_mask == nullptr || (r0 + r < rows && row_mask[r0 + r] != 0);
         const float y = round_bf16(acc[jj] + bias);  // nn.Linear output boundary
         bf16_t* px = sX + r * kLdD + col;
-        if (keep) *px = f32_to_bf16(bf16_to_f32(*px) + y);
+        const bf16_t old = *px;
+        *px = keep[jj] ? f32_to_bf16(bf16_to_f32(old) + y) : old;
       }
     }
     __syncthreads();
@@ -193,9 +228,8 @@ block_tail_kernel(const bf16_t* __restrict__ ctx, const bf16_t* __restrict__ x, 
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
         const int r = 4 * g + jj;
-        const bool keep = row_mask == nullptr || (r0 + r < rows && row_mask[r0 + r] != 0);
         const float y = round_bf16(acc[jj] + bias);
-        sA[r * kLdD + col] = keep ? f32_to_bf16(bf16_to_f32(sX[r * kLdD + col]) + y) : bf16_t(0);
+        sA[r * kLdD + col] = keep[jj] ? f32_to_bf16(bf16_to_f32(sX[r * kLdD + col]) + y) : bf16_t(0);
       }
     }
     __syncthreads();
