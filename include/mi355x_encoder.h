@@ -147,6 +147,10 @@ int enc_mask_lengths(const uint8_t* mask, int64_t batch, int64_t seq_len,
 
 /* flags of enc_encoder_forward_bf16 */
 #define ENC_FWD_ONLINE_ATTENTION 1 /* one-pass online-softmax attention      */
+#define ENC_FWD_SKIP_FINAL_NORM 2  /* out = last block's output: the caller
+                                      runs final_norm (enc_layernorm_bf16,
+                                      with row_mask), e.g. into a fresh
+                                      tensor after a graph replay           */
 
 /* Bytes of device workspace enc_encoder_forward_bf16 needs for this shape. */
 int64_t enc_encoder_workspace_bytes(int64_t batch, int64_t seq_len,
@@ -165,7 +169,10 @@ int64_t enc_encoder_workspace_bytes(int64_t batch, int64_t seq_len,
  * padded rows (models.py:736-737) and so is the final output
  * (models.py:917-918).  kv_len / key_mask are passed to the attention as in
  * enc_attention_fwd_bf16 (at most one of them non-null).  x is not modified;
- * out may not alias x or the workspace.  flags: 0 or ENC_FWD_ONLINE_ATTENTION.
+ * out may not alias x or the workspace.  flags: ENC_FWD_ONLINE_ATTENTION and/or
+ * ENC_FWD_SKIP_FINAL_NORM (no counterpart in the reference: it lets a graph
+ * replay end at a static buffer while the final norm writes the fresh output
+ * tensor the reference's graph path returns as a clone, models.py:1163-1239).
  * Replaces UserOptimizedTransformer.forward / _forward_eager
  * (transformer_benchmark/models.py:1020-1049, 1202-1239) and the block
  * forward (models.py:772-892). */

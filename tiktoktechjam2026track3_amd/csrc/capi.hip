@@ -254,7 +254,10 @@ int enc_encoder_forward_bf16(const void* x, void* out, void* workspace, int64_t 
                              int64_t num_heads, int64_t ffn_dim, int64_t num_layers, float eps, int32_t causal,
                              const int32_t* kv_len, const uint8_t* key_mask, const uint8_t* row_mask,
                              int32_t flags, void* stream) {
-  if (flags & ~ENC_FWD_ONLINE_ATTENTION) return fail(ENC_ERR_INVALID, "encoder: unknown flags");
+  if (flags & ~(ENC_FWD_ONLINE_ATTENTION | ENC_FWD_SKIP_FINAL_NORM))
+    return fail(ENC_ERR_INVALID, "encoder: unknown flags");
+  const bool final_norm = (flags & ENC_FWD_SKIP_FINAL_NORM) == 0;
+  if (!final_norm && num_layers < 1) return fail(ENC_ERR_INVALID, "encoder: skipping final_norm needs a layer");
   const bool exact = (flags & ENC_FWD_ONLINE_ATTENTION) == 0;
   int rc = check_encoder_shape(batch, seq_len, d_model, num_heads, ffn_dim, exact);
   if (rc != ENC_OK) return rc;
@@ -334,11 +337,11 @@ int enc_encoder_forward_bf16(const void* x, void* out, void* workspace, int64_t 
       ta.b1 = W(layer, 9);
       ta.w2 = W(layer, 10);
       ta.b2 = W(layer, 11);
-      ta.out = x_attn;
+      ta.out = (!final_norm && layer == num_layers - 1) ? static_cast<bf16_t*>(out) : x_attn;
       ta.row_mask = row_mask;
       e = enc::block_tail_bf16(ta, T, D, F, eps, cus, st);
       if (e != hipSuccess) return fail_hip(e, "encoder block tail");
-      cur = x_attn;
+      cur = ta.out;
       continue;
     }
     // out_proj + residual; padded rows keep the residual (attention output is 0 there)
@@ -359,7 +362,7 @@ int enc_encoder_forward_bf16(const void* x, void* out, void* workspace, int64_t 
     e = enc::gemm_bf16(ln, W(layer, 8), T, F, D, enc::kEpiBiasGelu, fa, cus, st);
     if (e != hipSuccess) return fail_hip(e, "encoder ffn_in");
     // ffn_out + residual; padded rows are zeroed (block output masked_fill)
-    bf16_t* x_next = (x_attn == xa) ? xb : xa;
+    bf16_t* x_next = (!final_norm && layer == num_layers - 1) ? static_cast<bf16_t*>(out) : (x_attn == xa) ? xb : xa;
     enc::GemmEpilogueArgs fo;
     fo.bias = W(layer, 11);
     fo.residual = x_attn;
@@ -369,6 +372,7 @@ int enc_encoder_forward_bf16(const void* x, void* out, void* workspace, int64_t 
     if (e != hipSuccess) return fail_hip(e, "encoder ffn_out");
     cur = x_next;
   }
+  if (!final_norm) return ok();  // out holds the last block's output
   e = enc::layernorm_bf16(cur, static_cast<const bf16_t*>(weights[12 * num_layers]),
                           static_cast<const bf16_t*>(weights[12 * num_layers + 1]), static_cast<bf16_t*>(out), T, D,
                           eps, row_mask, st);

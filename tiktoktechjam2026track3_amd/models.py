@@ -378,6 +378,10 @@ class UserOptimizedTransformer(BaselineTransformer):
         self._cuda_graph_stream: Optional[torch.cuda.Stream] = None
         self._cuda_graph_signature: Optional[Tuple[object, ...]] = None
         self._cuda_graph_capture_count = 0
+        # A captured graph ends at the last block's output; each call applies
+        # final_norm from it into a fresh tensor (row mask of the capture).
+        self._cuda_graph_final_norm = False
+        self._cuda_graph_row_mask: Optional[torch.Tensor] = None
         self._mask_cache_entry: Optional[_MaskCacheEntry] = None
 
     # ---- mask classification (cached per tensor version, models.py:1122-1161) ----
@@ -513,6 +517,7 @@ class UserOptimizedTransformer(BaselineTransformer):
         x: torch.Tensor,
         valid_token_mask: Optional[torch.Tensor],
         mask_kind: str,
+        final_norm: bool = True,
     ) -> torch.Tensor:
         from . import native
 
@@ -533,7 +538,24 @@ class UserOptimizedTransformer(BaselineTransformer):
         native.encoder_forward(
             x, out, workspace, table, cfg.num_heads, cfg.ffn_dim, cfg.num_layers, eps,
             cfg.causal, kv_len, key_mask, row_mask, online_attention=self.online_attention,
+            final_norm=final_norm,
         )
+        return out
+
+    def _graph_result(self) -> torch.Tensor:
+        """A fresh tensor with the replayed graph's output (the reference's
+        graph path returns a clone, models.py:1163-1239).  Graphs captured by
+        this module stop before final_norm, which then writes the fresh tensor
+        directly instead of a copy following it."""
+        static = self._cuda_graph_output
+        assert static is not None
+        if not self._cuda_graph_final_norm:
+            return static.clone()
+        from . import native
+
+        out = torch.empty_like(static)
+        norm = self.final_norm
+        native.layernorm(static, norm.weight, norm.bias, norm.eps, out=out, row_mask=self._cuda_graph_row_mask)
         return out
 
     # ---- HIP graph replay for launch-bound shapes ----
@@ -588,6 +610,7 @@ class UserOptimizedTransformer(BaselineTransformer):
     ) -> torch.Tensor:
         self._cuda_graph = None
         self._cuda_graph_output = None
+        self._cuda_graph_final_norm = False
         self._cuda_graph_stream = None
         self._cuda_graph_signature = None
 
@@ -596,23 +619,28 @@ class UserOptimizedTransformer(BaselineTransformer):
         capture_stream.wait_stream(replay_stream)
         with torch.cuda.stream(capture_stream), torch.inference_mode():
             for _ in range(2):
-                self._forward_native(x, valid_token_mask, mask_kind)
+                self._forward_native(x, valid_token_mask, mask_kind, final_norm=False)
         replay_stream.wait_stream(capture_stream)
         torch.cuda.synchronize(x.device)
 
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, stream=capture_stream):
-            graph_output = self._forward_native(x, valid_token_mask, mask_kind)
+            graph_output = self._forward_native(x, valid_token_mask, mask_kind, final_norm=False)
+        row_mask = None
+        if valid_token_mask is not None and mask_kind != MASK_ALL_TRUE:
+            row_mask = valid_token_mask.contiguous().view(torch.uint8)
 
         self._cuda_graph = graph
         self._cuda_graph_output = graph_output
         self._cuda_graph_stream = capture_stream
         self._cuda_graph_signature = signature
+        self._cuda_graph_final_norm = True
+        self._cuda_graph_row_mask = row_mask
         self._cuda_graph_capture_count += 1
         if self._cuda_graph_capture_count == 1:
             print(f"[optimized] captured HIP graph for shape={tuple(x.shape)}")
         graph.replay()
-        return graph_output.clone()
+        return self._graph_result()
 
     # ---- entry point ----
 
@@ -637,7 +665,7 @@ class UserOptimizedTransformer(BaselineTransformer):
             return self._capture_cuda_graph(x, valid_token_mask, mask_kind, signature)
         assert self._cuda_graph is not None and self._cuda_graph_output is not None
         self._cuda_graph.replay()
-        return self._cuda_graph_output.clone()
+        return self._graph_result()
 
 
 def copy_model_weights(baseline: nn.Module, optimized: nn.Module, strict: bool = True) -> None:

@@ -28,6 +28,7 @@ ENC_ERR_HIP = 3
 ENC_ERR_OOM = 4
 
 ENC_FWD_ONLINE_ATTENTION = 1
+ENC_FWD_SKIP_FINAL_NORM = 2
 
 ENC_EPI_BIAS = 0
 ENC_EPI_BIAS_GELU = 1
@@ -317,12 +318,16 @@ def encoder_forward(
     key_mask: Optional[torch.Tensor],
     row_mask: Optional[torch.Tensor],
     online_attention: bool = False,
+    final_norm: bool = True,
 ) -> None:
     """Run the whole encoder through enc_encoder_forward_bf16.
 
     ``weight_table`` is a CPU int64 tensor of device pointers in the order the
-    C ABI documents; ``key_mask``/``row_mask`` are uint8 [B, S] tensors.
+    C ABI documents; ``key_mask``/``row_mask`` are uint8 [B, S] tensors.  With
+    ``final_norm=False`` ``out`` receives the last block's output and the
+    caller applies final_norm (ENC_FWD_SKIP_FINAL_NORM).
     """
+    flags = (ENC_FWD_ONLINE_ATTENTION if online_attention else 0) | (0 if final_norm else ENC_FWD_SKIP_FINAL_NORM)
     batch, seq_len, d_model = x.shape
     table = ctypes.cast(weight_table.data_ptr(), ctypes.c_void_p)
     _check(
@@ -331,6 +336,6 @@ def encoder_forward(
             x.data_ptr(), out.data_ptr(), workspace.data_ptr(), workspace.numel(), table.value,
             batch, seq_len, d_model, num_heads, ffn_dim, num_layers, float(eps), int(bool(causal)),
             _ptr(kv_len), _ptr(key_mask), _ptr(row_mask),
-            ENC_FWD_ONLINE_ATTENTION if online_attention else 0, _stream(x.device),
+            flags, _stream(x.device),
         ),
     )
