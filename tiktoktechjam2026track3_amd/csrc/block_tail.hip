@@ -84,7 +84,8 @@ block_tail_kernel(const bf16_t* __restrict__ ctx, const bf16_t* __restrict__ x, 
                   const bf16_t* __restrict__ bo, const bf16_t* __restrict__ g2, const bf16_t* __restrict__ be2,
                   const bf16_t* __restrict__ w1, const bf16_t* __restrict__ b1, const bf16_t* __restrict__ w2,
                   const bf16_t* __restrict__ b2, bf16_t* __restrict__ out, int rows, float eps,
-                  const uint8_t* __restrict__ row_mask) {
+                  const uint8_t* __restrict__ row_mask, const bf16_t* __restrict__ g1n,
+                  const bf16_t* __restrict__ be1n, bf16_t* __restrict__ ln_out) {
   static_assert((D == 32 || D == 64 || D == 128) && (F == 32 || F == 64 || F == 128), "d_model, ffn_dim");
   constexpr int kLdD = tail_ld(D), kLdF = tail_ld(F);
   constexpr int kSlabChunks = kTailRows * (D / 8);  // 16-byte chunks of a [16][D] slab
@@ -122,6 +123,13 @@ block_tail_kernel(const bf16_t* __restrict__ ctx, const bf16_t* __restrict__ x, 
   const int seg = lane / L, j = lane % L;
   const u32x2 gw = *reinterpret_cast<const u32x2*>(g2 + 4 * j);
   const u32x2 bw = *reinterpret_cast<const u32x2*>(be2 + 4 * j);
+  // the next layer's norm1 (optional: ln_out == nullptr skips it)
+  const bool next_norm = ln_out != nullptr;
+  u32x2 gn = {0u, 0u}, bn = {0u, 0u};
+  if (next_norm) {
+    gn = *reinterpret_cast<const u32x2*>(g1n + 4 * j);
+    bn = *reinterpret_cast<const u32x2*>(be1n + 4 * j);
+  }
 
   // the slab's context and residual chunks travel in registers one slab ahead
   const int slabs = (rows + kTailRows - 1) / kTailRows;
@@ -238,6 +246,28 @@ block_tail_kernel(const bf16_t* __restrict__ ctx, const bf16_t* __restrict__ x, 
     if (has_chunk && r0 + my_r < rows)
       *reinterpret_cast<u32x4*>(out + static_cast<int64_t>(r0 + my_r) * D + my_ch * 8) =
           *reinterpret_cast<const u32x4*>(sA + my_r * kLdD + my_ch * 8);
+
+    // ---- the next layer's norm1 of the block output rows (no row mask, as
+    // the separate launch) -> ln_out ----
+    if (next_norm) {
+      for (int p = 0; p < kTailRows; p += 4 * R) {
+        const int r = p + wave * R + seg;
+        const int rr = r < kTailRows ? r : kTailRows - 1;  // lanes past the slab only join the shuffles
+        const u32x2 w = *reinterpret_cast<const u32x2*>(sA + rr * kLdD + 4 * j);
+        const float v[4] = {lo_bf16(w[0]), hi_bf16(w[0]), lo_bf16(w[1]), hi_bf16(w[1])};
+        float mean, rstd;
+        packed_row_stats<L>(v, j, seg, eps, &mean, &rstd);
+        if (r < kTailRows && r0 + r < rows) {
+          const float ga[4] = {lo_bf16(gn[0]), hi_bf16(gn[0]), lo_bf16(gn[1]), hi_bf16(gn[1])};
+          const float be[4] = {lo_bf16(bn[0]), hi_bf16(bn[0]), lo_bf16(bn[1]), hi_bf16(bn[1])};
+          float o[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o[e] = fmaf(ga[e], rstd * (v[e] - mean), be[e]);
+          *reinterpret_cast<u32x2*>(ln_out + static_cast<int64_t>(r0 + r) * D + 4 * j) =
+              u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+        }
+      }
+    }
   }
 }
 
@@ -255,7 +285,7 @@ hipError_t launch_tail(const BlockTailArgs& a, int rows, float eps, int num_cus,
   const int slabs = (rows + kTailRows - 1) / kTailRows;
   const int grid = slabs < num_cus ? slabs : num_cus;
   hipLaunchKernelGGL(kernel, dim3(grid), dim3(kTailThreads), kLds, st, a.ctx, a.x, a.wo, a.bo, a.g2, a.be2, a.w1,
-                     a.b1, a.w2, a.b2, a.out, rows, eps, a.row_mask);
+                     a.b1, a.w2, a.b2, a.out, rows, eps, a.row_mask, a.g1n, a.be1n, a.ln_out);
   return hipGetLastError();
 }
 

@@ -296,16 +296,20 @@ int enc_encoder_forward_bf16(const void* x, void* out, void* workspace, int64_t 
   // per CU cannot hide its per-slab latency; measured on MI355X.)
   bool tail_fused = enc::block_tail_supported(D, F) && T <= 8192;
   for (int64_t layer = 0; tail_fused && layer < num_layers; ++layer)
-    for (int idx = 4; idx < 12; ++idx)
-      tail_fused = tail_fused && reinterpret_cast<uintptr_t>(W(layer, idx)) % 16 == 0;
+    for (int idx = 0; idx < 12; ++idx)
+      tail_fused = tail_fused && (idx == 2 || idx == 3 || reinterpret_cast<uintptr_t>(W(layer, idx)) % 16 == 0);
 
   const bf16_t* cur = static_cast<const bf16_t*>(x);
   hipError_t e = hipSuccess;
+  bool ln_ready = false;  // the fused tail already wrote this layer's norm1
   for (int64_t layer = 0; layer < num_layers; ++layer) {
     bf16_t* x_attn = (cur == xa) ? xb : xa;  // residual stream after attention
     // norm1
-    e = enc::layernorm_bf16(cur, W(layer, 0), W(layer, 1), ln, T, D, eps, nullptr, st);
-    if (e != hipSuccess) return fail_hip(e, "encoder norm1");
+    if (!ln_ready) {
+      e = enc::layernorm_bf16(cur, W(layer, 0), W(layer, 1), ln, T, D, eps, nullptr, st);
+      if (e != hipSuccess) return fail_hip(e, "encoder norm1");
+    }
+    ln_ready = false;
     // packed QKV, head-major
     enc::GemmEpilogueArgs qa;
     qa.bias = W(layer, 3);
@@ -339,6 +343,12 @@ int enc_encoder_forward_bf16(const void* x, void* out, void* workspace, int64_t 
       ta.b2 = W(layer, 11);
       ta.out = (!final_norm && layer == num_layers - 1) ? static_cast<bf16_t*>(out) : x_attn;
       ta.row_mask = row_mask;
+      if (layer + 1 < num_layers) {  // the next layer's norm1 comes with the tail
+        ta.g1n = W(layer + 1, 0);
+        ta.be1n = W(layer + 1, 1);
+        ta.ln_out = ln;
+        ln_ready = true;
+      }
       e = enc::block_tail_bf16(ta, T, D, F, eps, cus, st);
       if (e != hipSuccess) return fail_hip(e, "encoder block tail");
       cur = ta.out;

@@ -98,6 +98,11 @@ struct BlockTailArgs {
   const bf16_t* b2 = nullptr;
   bf16_t* out = nullptr;        // block output [T, D]; may alias x
   const uint8_t* row_mask = nullptr;
+  // optional: the next layer's norm1 (weight, bias) applied to the block
+  // output, written to ln_out [T, D] (no row mask, as the separate launch)
+  const bf16_t* g1n = nullptr;
+  const bf16_t* be1n = nullptr;
+  bf16_t* ln_out = nullptr;
 };
 bool block_tail_supported(int64_t d_model, int64_t ffn_dim);
 hipError_t block_tail_bf16(const BlockTailArgs& args, int64_t rows, int64_t d_model, int64_t ffn_dim, float eps,
