@@ -9,8 +9,10 @@
 // matrices fit in LDS together (104 KB at 128 / 128), so one persistent
 // workgroup per CU loads them once and walks 16-row slabs of the tokens: the
 // context and residual rows come in, every intermediate stays in LDS, and
-// only x_out goes out.  For these sizes the products are latency-bound and the
-// three launches it saves per layer matter more than MFMA rate.
+// only x_out goes out (with, optionally, the next layer's norm1 of the same
+// rows).  For these sizes the products are latency-bound and the launches it
+// saves per layer (three, four with the next norm1) matter more than MFMA
+// rate.
 //
 // The arithmetic is the wide path's, operation for operation, so the output
 // is bitwise the same: each product accumulates K sequentially in 16-deep

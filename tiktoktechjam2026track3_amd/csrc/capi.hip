@@ -291,7 +291,8 @@ int enc_encoder_forward_bf16(const void* x, void* out, void* workspace, int64_t 
   auto W = [&](int64_t layer, int idx) { return static_cast<const bf16_t*>(weights[layer * 12 + idx]); };
 
   // Narrow models with up to 8192 tokens run the block tail (out_proj ..
-  // ffn_out) as one kernel, whose 16-byte loads need 16-byte aligned weights.
+  // ffn_out, and the next layer's norm1) as one kernel, whose 16-byte loads
+  // need 16-byte aligned weights (all but the QKV projection's).
   // (With more tokens the four launches win: the fused kernel's one workgroup
   // per CU cannot hide its per-slab latency; measured on MI355X.)
   bool tail_fused = enc::block_tail_supported(D, F) && T <= 8192;
