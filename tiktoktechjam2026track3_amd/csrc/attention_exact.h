@@ -473,6 +473,23 @@ attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
     const bool tiny = (mn != INFINITY) && (to_score(mn) - row_max < kMinFastGap);
     slow_div = __builtin_amdgcn_ballot_w64(tiny) != 0;
   }
+  // Gaps -> weights exp(gap) in place (short-row regime).  Without the fast
+  // division verdict's exception (slow_div) every allowed key's gap is at
+  // least kMinFastGap, and a tile with no excluded key holds no -inf, so the
+  // underflow clamp (below -103.28) cannot fire there and is left out.
+  auto tile_exp = [&](f32x16 (&s)[2], bool clamp) {
+    if (clamp) {
+#pragma unroll
+      for (int kb32 = 0; kb32 < 2; ++kb32)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[kb32][r] = expf_nonpos(s[kb32][r]);
+    } else {
+#pragma unroll
+      for (int kb32 = 0; kb32 < 2; ++kb32)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[kb32][r] = expf_nonpos_unclamped(s[kb32][r]);
+    }
+  };
 
   // ======================= sweep B: row sum of exp(s - max) =======================
   float row_sum;
@@ -488,10 +505,7 @@ attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
       // this wavefront's weights, zeros for a tile no query of the block sees
       if (wave < active) {
         dots_to_gaps(wave, wave * kBKV, row_max, raw_max_bf, true, cache[0]);
-#pragma unroll
-        for (int kb32 = 0; kb32 < 2; ++kb32)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) cache[0][kb32][r] = expf_nonpos(cache[0][kb32][r]);
+        tile_exp(cache[0], slow_div || tile_needs_mask(wave * kBKV));
       } else {
 #pragma unroll
         for (int kb32 = 0; kb32 < 2; ++kb32)
@@ -515,23 +529,22 @@ attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
       for (int t = 0; t < 2; ++t) {
         if (t >= active) continue;
         dots_to_gaps(t, t * kBKV, row_max, raw_max_bf, true, cache[t]);
+        tile_exp(cache[t], slow_div || tile_needs_mask(t * kBKV));
 #pragma unroll
         for (int kb32 = 0; kb32 < 2; ++kb32)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            cache[t][kb32][r] = expf_nonpos(cache[t][kb32][r]);
-            part[kb32][r] += cache[t][kb32][r];
-          }
+          for (int r = 0; r < 16; ++r) part[kb32][r] += cache[t][kb32][r];
       }
     } else {
       sweep(natural, false, active, [&](int buf, int kb) {
         const int k0 = kb * kBKV;
         f32x16 s[2];
         tile_gaps(buf, k0, row_max, raw_max_bf, true, s);
+        tile_exp(s, slow_div || tile_needs_mask(k0));
 #pragma unroll
         for (int kb32 = 0; kb32 < 2; ++kb32)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) part[kb32][r] += expf_nonpos(s[kb32][r]);
+          for (int r = 0; r < 16; ++r) part[kb32][r] += s[kb32][r];
       });
     }
     // 64-lane butterfly; lam bits: 5 = kb32, 4 = i>>1 (reg bit 3), 3 = lane half,
@@ -706,7 +719,12 @@ attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
     sweep(natural, true, active, [&](int buf, int kb) {
       f32x16 s[2];
       tile_gaps(buf, kb * kBKV, row_max, raw_max_bf, !BLOCK_ORDER, s);
-      pv_body(buf, s, false);
+      if (!BLOCK_ORDER && !slow_div) {
+        tile_exp(s, tile_needs_mask(kb * kBKV));
+        pv_body(buf, s, true);
+      } else {
+        pv_body(buf, s, false);
+      }
     });
   }
 
