@@ -412,7 +412,20 @@ attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
   // ============================ sweep A: row max ============================
   // max (and, for the short-row regime, min) of the raw dot products of the
   // allowed keys; the bf16 score of the max is formed once afterwards.
+  // Long rows use the NaN-propagating maximum (v_maximum3_f32), which needs
+  // no NaN-quieting copy of each MFMA result as fmaxf does; for numbers the
+  // two agree except in the sign of a zero max, which changes no gap's value
+  // (s - (+0) = s - (-0), and exp(-0) = exp(+0) = 1).  (Short rows keep
+  // fmaxf / fminf: measured faster there.)
   float mx = -INFINITY, mn = INFINITY;
+  auto vmax = [](float a, float b) {
+    if constexpr (BLOCK_ORDER) {
+      return __builtin_elementwise_maximum(a, b);
+    } else {
+      return fmaxf(a, b);
+    }
+  };
+  auto vmin = [](float a, float b) { return fminf(a, b); };
   auto max_body = [&](int buf, int kb, f32x16 (&s)[2]) {
     const int k0 = kb * kBKV;
     tile_dots(buf, s);
@@ -422,15 +435,15 @@ attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const bool ok = key_ok(buf, k0, tile_key(kb32, r, lhi));
-          mx = fmaxf(mx, ok ? s[kb32][r] : -INFINITY);
-          if constexpr (!BLOCK_ORDER) mn = fminf(mn, ok ? s[kb32][r] : INFINITY);
+          mx = vmax(mx, ok ? s[kb32][r] : -INFINITY);
+          if constexpr (!BLOCK_ORDER) mn = vmin(mn, ok ? s[kb32][r] : INFINITY);
         }
       }
     } else {
 #pragma unroll
       for (int r = 0; r < 16; r += 2) {
-        mx = fmaxf(mx, fmaxf(fmaxf(s[0][r], s[0][r + 1]), fmaxf(s[1][r], s[1][r + 1])));
-        if constexpr (!BLOCK_ORDER) mn = fminf(mn, fminf(fminf(s[0][r], s[0][r + 1]), fminf(s[1][r], s[1][r + 1])));
+        mx = vmax(mx, vmax(vmax(s[0][r], s[0][r + 1]), vmax(s[1][r], s[1][r + 1])));
+        if constexpr (!BLOCK_ORDER) mn = vmin(mn, vmin(vmin(s[0][r], s[0][r + 1]), vmin(s[1][r], s[1][r + 1])));
       }
     }
   };
