@@ -416,7 +416,7 @@ attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
   // no NaN-quieting copy of each MFMA result as fmaxf does; for numbers the
   // two agree except in the sign of a zero max, which changes no gap's value
   // (s - (+0) = s - (-0), and exp(-0) = exp(+0) = 1).  (Short rows keep
-  // fmaxf / fminf: measured faster there.)
+  // fmaxf / fminf: no gain was measured there.)
   float mx = -INFINITY, mn = INFINITY;
   auto vmax = [](float a, float b) {
     if constexpr (BLOCK_ORDER) {
