@@ -1013,15 +1013,17 @@ hipError_t launch_big(const bf16_t* A, const bf16_t* W, int M, int N, int K, int
 // lane), the residual / outputs too (16-byte epilogue stores), and the tile
 // count should fill the device's CUs.
 int pick_big_tile(int64_t M, int64_t N, const bf16_t* A, const bf16_t* W, const GemmEpilogueArgs& ep,
-                  bool ep_is_gelu, int num_cus) {
+                  bool ep_overlaps, int num_cus) {
   auto al = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
   if (!al(A) || !al(W) || !al(ep.out) || !al(ep.residual) || !al(ep.q) || !al(ep.k) || !al(ep.v_t)) return 0;
   if (M < 1024) return 0;
   const int64_t t256x128 = ((M + 255) / 256) * (N / 128);
-  // The erf GELU epilogue is long dependent VALU work; with two resident
-  // 256x128 tiles per CU one tile's epilogue overlaps the other's MFMA loop
-  // (when there are tiles for two per CU: a narrow N leaves most CUs idle).
-  if (ep_is_gelu && N % 128 == 0 && t256x128 >= 2 * num_cus) return 256129;
+  // With two resident 256x128 tiles per CU one tile's epilogue overlaps the
+  // other's MFMA loop (when there are tiles for two per CU: a narrow N leaves
+  // most CUs idle).  It pays where the epilogue is long against the K loop:
+  // the erf GELU (long dependent VALU work), and the residual epilogues at
+  // K <= 1024 (32768x1024x1024: 88 vs 95 us; at K = 4096 it is slower).
+  if (ep_overlaps && N % 128 == 0 && t256x128 >= 2 * num_cus) return 256129;
   // Whole rounds of tiles over the CUs times the tile's work, over its
   // measured per-tile efficiency (256x128 tiles run ~10% below 256x256).
   auto cost = [&](int bm, int bn, double eff) {
@@ -1119,7 +1121,9 @@ hipError_t gemm_bf16(const bf16_t* A, const bf16_t* W, int64_t M, int64_t N, int
   if (split == 4 && chunk == 32) return launch_split<4, 32>(A, W, m, n, k, epi, ep, stream);
   if (split == 4 && chunk == 64) return launch_split<4, 64>(A, W, m, n, k, epi, ep, stream);
   if (split == 2 && chunk == 128) return launch_split<2, 128>(A, W, m, n, k, epi, ep, stream);
-  switch (pick_big_tile(M, N, A, W, ep, epi == kEpiBiasGelu, num_cus)) {
+  const bool residual = epi == kEpiResidualKeep || epi == kEpiResidualZero;
+  const bool ep_overlaps = epi == kEpiBiasGelu || (residual && K <= 1024);
+  switch (pick_big_tile(M, N, A, W, ep, ep_overlaps, num_cus)) {
     case 256129: return launch_big<256, 128, 32, 3, 2>(A, W, m, n, k, epi, ep, stream);
     case 256256: return launch_big<256, 256, 32, 4>(A, W, m, n, k, epi, ep, stream);
     case 256128: return launch_big<256, 128, 64, 3>(A, W, m, n, k, epi, ep, stream);
