@@ -183,6 +183,32 @@ def test_graph_replay_matches_eager(device):
         assert compare(ref, replayed, RTOL, ATOL)["passed"]
 
 
+def test_graph_survives_eager_call_at_another_shape(device):
+    """A call at another sequence length runs eagerly and replaces the eager
+    workspace; the captured graph must keep writing its own buffers, so the
+    next replay at the captured shape still equals the eager forward."""
+    spec = ENCODER_CONFIGS["c2"]
+    cfg = spec.config
+    _, candidate = build_models(cfg, spec.seed, device)
+    with torch.inference_mode():
+        x, mask = generate_random_case(cfg, device, torch.bfloat16, 11, 0.0, 1.0)
+        candidate(x, mask)  # capture
+        graph = candidate._cuda_graph
+        assert graph is not None
+        x_other = torch.randn(cfg.batch_size, cfg.seq_len + 64, cfg.d_model, device=device).bfloat16()
+        other = candidate(x_other)  # eager, new workspace size
+        torch.cuda.synchronize()
+        assert candidate._cuda_graph is graph  # no recapture for the other shape
+        filler = torch.full((64 * 1024 * 1024,), 7, dtype=torch.uint8, device=device)  # reuse freed memory
+        replayed = candidate(x, mask)
+        torch.cuda.synchronize()
+        assert candidate._cuda_graph is graph
+        eager = candidate._forward_native(x, mask, "all_true")
+        assert torch.equal(replayed, eager)
+        assert torch.equal(candidate._forward_native(x_other, None, "all_true"), other)
+        del filler
+
+
 def test_online_attention_encoder_stays_close(device):
     """The opt-in one-pass attention: its bf16 weight-rounding noise compounds
     over the layers, so it is held to a looser bound than the reference's gate
