@@ -186,6 +186,32 @@ int enc_encoder_forward_bf16(const void* x, void* out, void* workspace,
                              const uint8_t* row_mask, int32_t flags,
                              void* stream);
 
+/* Bytes of the library-owned scratch array behind
+ * enc_encoder_forward_bf16_noalloc (one array per GPU). */
+#define ENC_NOALLOC_SCRATCH_BYTES (64ll * 1024 * 1024)
+
+/* enc_encoder_forward_bf16 without a caller workspace and without any device
+ * allocation: the activation buffers live in a statically sized device array
+ * of ENC_NOALLOC_SCRATCH_BYTES that the library holds on every GPU it runs
+ * on until the process ends.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture
+ * that must not call hipMalloc, tight serving loops, harnesses that forbid
+ * allocation).  Same arguments, results and errors as
+ * enc_encoder_forward_bf16 otherwise; a shape whose workspace
+ * (enc_encoder_workspace_bytes) exceeds the array is rejected with
+ * ENC_ERR_UNSUPPORTED before anything is launched.  Every call on one GPU
+ * shares that GPU's array: calls that overlap in time on one GPU (other
+ * streams or threads) race and must be serialised by the caller. */
+int enc_encoder_forward_bf16_noalloc(const void* x, void* out,
+                                     const void* const* weights, int64_t batch,
+                                     int64_t seq_len, int64_t d_model,
+                                     int64_t num_heads, int64_t ffn_dim,
+                                     int64_t num_layers, float eps,
+                                     int32_t causal, const int32_t* kv_len,
+                                     const uint8_t* key_mask,
+                                     const uint8_t* row_mask, int32_t flags,
+                                     void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -261,3 +261,20 @@ def test_profiling_summary_reports_mfma_utilisation(tmp_path):
     assert profiling.main(["--trace", str(tmp_path / "trace"), "--mfma", str(tmp_path / "mfma"), "--workload", "cX",
                            "--label", "gemm=gemm_big_kernel<256, 128>", "--out", str(out)]) == 0
     assert "| gemm (`gemm_big_kernel<256, 128>`) | 2 | 50.0% |" in out.read_text()
+
+
+def test_noalloc_entry_point_rejects_large_shapes_before_any_device_call():
+    """The workspace-size check of enc_encoder_forward_bf16_noalloc runs before
+    any HIP call (here there is no GPU): a c3-sized forward needs more than the
+    library's scratch array."""
+    lib = native.load_library()
+    layers = 1
+    table = (ctypes.c_void_p * (12 * layers + 2))(*([1] * (12 * layers + 2)))
+    fake = ctypes.c_void_p(16)
+    rc = lib.enc_encoder_forward_bf16_noalloc(
+        fake, fake, ctypes.cast(table, ctypes.c_void_p), 8, 1024, 1024, 16, 4096, layers, 1e-5, 1,
+        None, None, None, 0, None,
+    )
+    assert rc == native.ENC_ERR_UNSUPPORTED
+    assert b"scratch array" in lib.enc_last_error()
+    assert lib.enc_encoder_workspace_bytes(8, 1024, 1024, 16, 4096) > native.NOALLOC_SCRATCH_BYTES

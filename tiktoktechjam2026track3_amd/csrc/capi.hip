@@ -7,6 +7,7 @@
 
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "../../include/mi355x_encoder.h"
@@ -50,6 +51,36 @@ int device_cus() {
 }
 
 inline int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
+
+// Library-owned activation workspace of enc_encoder_forward_bf16_noalloc: one
+// copy per GPU, loaded with the code object and held until the process ends.
+// In host code `scratch` names a host-side stand-in; kernels get the device
+// address kept in g_scratch_ptr, looked up once per device.
+constexpr int64_t kScratchBytes = ENC_NOALLOC_SCRATCH_BYTES;
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {nullptr};
+
+// Device address of this device's scratch array (looked up on the first call
+// per device, with that device current), or an error code.
+int scratch_for_current_device(void** ptr) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail_hip(e, "noalloc: hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(ENC_ERR_UNSUPPORTED, "noalloc: device ordinal out of range");
+  std::lock_guard<std::mutex> guard(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return fail_hip(e, "noalloc: hipGetSymbolAddress(scratch)");
+    if (p == nullptr) return fail(ENC_ERR_HIP, "noalloc: scratch has no device address");
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return ENC_OK;
+}
 
 // Workspace carve-up for the encoder forward.
 struct EncoderWorkspace {
@@ -102,6 +133,160 @@ int check_encoder_shape(int64_t B, int64_t S, int64_t D, int64_t H, int64_t F, b
   if (B * S >= (int64_t(1) << 31)) return fail(ENC_ERR_UNSUPPORTED, "batch * seq_len must be < 2^31");
   return ENC_OK;
 }
+
+}  // namespace
+
+namespace {
+
+// Argument checks shared by the two encoder entry points; on success *plan
+// holds the workspace carve-up for the shape.
+int check_encoder_call(const void* x, void* out, const void* const* weights, int64_t batch, int64_t seq_len,
+                       int64_t d_model, int64_t num_heads, int64_t ffn_dim, int64_t num_layers, float eps,
+                       const int32_t* kv_len, const uint8_t* key_mask, int32_t flags, EncoderWorkspace* plan) {
+  if (flags & ~(ENC_FWD_ONLINE_ATTENTION | ENC_FWD_SKIP_FINAL_NORM))
+    return fail(ENC_ERR_INVALID, "encoder: unknown flags");
+  const bool final_norm = (flags & ENC_FWD_SKIP_FINAL_NORM) == 0;
+  if (!final_norm && num_layers < 1) return fail(ENC_ERR_INVALID, "encoder: skipping final_norm needs a layer");
+  const bool exact = (flags & ENC_FWD_ONLINE_ATTENTION) == 0;
+  int rc = check_encoder_shape(batch, seq_len, d_model, num_heads, ffn_dim, exact);
+  if (rc != ENC_OK) return rc;
+  if (num_layers < 0) return fail(ENC_ERR_INVALID, "encoder: num_layers must be >= 0");
+  if (!x || !out || !weights) return fail(ENC_ERR_INVALID, "encoder: null pointer");
+  if (kv_len && key_mask) return fail(ENC_ERR_INVALID, "encoder: pass kv_len or key_mask, not both");
+  if (!(eps > 0.f)) return fail(ENC_ERR_INVALID, "encoder: eps must be positive");
+  for (int64_t i = 0; i < 12 * num_layers + 2; ++i)
+    if (!weights[i]) return fail(ENC_ERR_INVALID, "encoder: null weight pointer at index " + std::to_string(i));
+  *plan = plan_workspace(batch, seq_len, d_model, num_heads, ffn_dim);
+  return ENC_OK;
+}
+
+// The launch sequence of the encoder forward over a workspace laid out as `w`.
+int run_encoder_forward(const void* x, void* out, void* workspace, const EncoderWorkspace& w,
+                        const void* const* weights, int64_t batch, int64_t seq_len, int64_t d_model,
+                        int64_t num_heads, int64_t ffn_dim, int64_t num_layers, float eps, int32_t causal,
+                        const int32_t* kv_len, const uint8_t* key_mask, const uint8_t* row_mask, int32_t flags,
+                        void* stream) {
+  const bool final_norm = (flags & ENC_FWD_SKIP_FINAL_NORM) == 0;
+  const bool exact = (flags & ENC_FWD_ONLINE_ATTENTION) == 0;
+  using enc::bf16_t;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  char* base = static_cast<char*>(workspace);
+  bf16_t* ln = reinterpret_cast<bf16_t*>(base + w.ln);
+  bf16_t* q = reinterpret_cast<bf16_t*>(base + w.q);
+  bf16_t* k = reinterpret_cast<bf16_t*>(base + w.k);
+  bf16_t* vt = reinterpret_cast<bf16_t*>(base + w.vt);
+  bf16_t* ctx = reinterpret_cast<bf16_t*>(base + w.ctx);
+  bf16_t* xa = reinterpret_cast<bf16_t*>(base + w.xa);
+  bf16_t* xb = reinterpret_cast<bf16_t*>(base + w.xb);
+  bf16_t* hidden = reinterpret_cast<bf16_t*>(base + w.hidden);
+
+  const int64_t T = batch * seq_len;
+  const int64_t D = d_model, F = ffn_dim, H = num_heads;
+  const int cus = device_cus();
+  const float scale = 1.0f / sqrtf(static_cast<float>(D / H));
+  auto W = [&](int64_t layer, int idx) { return static_cast<const bf16_t*>(weights[layer * 12 + idx]); };
+
+  // Narrow models with up to 8192 tokens run the block tail (out_proj ..
+  // ffn_out, and the next layer's norm1) as one kernel, whose 16-byte loads
+  // need 16-byte aligned weights (all but the QKV projection's).
+  // (With more tokens the four launches win: the fused kernel's one workgroup
+  // per CU cannot hide its per-slab latency; measured on MI355X.)
+  bool tail_fused = enc::block_tail_supported(D, F) && T <= 8192;
+  for (int64_t layer = 0; tail_fused && layer < num_layers; ++layer)
+    for (int idx = 0; idx < 12; ++idx)
+      tail_fused = tail_fused && (idx == 2 || idx == 3 || reinterpret_cast<uintptr_t>(W(layer, idx)) % 16 == 0);
+
+  const bf16_t* cur = static_cast<const bf16_t*>(x);
+  hipError_t e = hipSuccess;
+  bool ln_ready = false;  // the fused tail already wrote this layer's norm1
+  for (int64_t layer = 0; layer < num_layers; ++layer) {
+    bf16_t* x_attn = (cur == xa) ? xb : xa;  // residual stream after attention
+    // norm1
+    if (!ln_ready) {
+      e = enc::layernorm_bf16(cur, W(layer, 0), W(layer, 1), ln, T, D, eps, nullptr, st);
+      if (e != hipSuccess) return fail_hip(e, "encoder norm1");
+    }
+    ln_ready = false;
+    // packed QKV, head-major
+    enc::GemmEpilogueArgs qa;
+    qa.bias = W(layer, 3);
+    qa.q = q;
+    qa.k = k;
+    qa.v_t = vt;
+    qa.seq_len = static_cast<int>(seq_len);
+    qa.num_heads = static_cast<int>(H);
+    qa.head_dim = static_cast<int>(D / H);
+    qa.d_model = static_cast<int>(D);
+    qa.ld_vt = static_cast<int>(enc::vt_stride(seq_len));
+    e = enc::gemm_bf16(ln, W(layer, 2), T, 3 * D, D, enc::kEpiQkvHeadMajor, qa, cus, st);
+    if (e != hipSuccess) return fail_hip(e, "encoder qkv");
+    // attention -> context [T, D]
+    auto attention = exact ? enc::attention_fwd_bf16 : enc::flash_attention_fwd_bf16;
+    e = attention(q, k, vt, ctx, static_cast<int>(batch), static_cast<int>(H), static_cast<int>(seq_len),
+                  static_cast<int>(D / H), scale, causal != 0, kv_len, key_mask, st);
+    if (e != hipSuccess) return fail_hip(e, "encoder attention");
+    if (tail_fused) {
+      // out_proj .. ffn_out in one launch (narrow models), same arithmetic
+      enc::BlockTailArgs ta;
+      ta.ctx = ctx;
+      ta.x = cur;
+      ta.wo = W(layer, 4);
+      ta.bo = W(layer, 5);
+      ta.g2 = W(layer, 6);
+      ta.be2 = W(layer, 7);
+      ta.w1 = W(layer, 8);
+      ta.b1 = W(layer, 9);
+      ta.w2 = W(layer, 10);
+      ta.b2 = W(layer, 11);
+      ta.out = (!final_norm && layer == num_layers - 1) ? static_cast<bf16_t*>(out) : x_attn;
+      ta.row_mask = row_mask;
+      if (layer + 1 < num_layers) {  // the next layer's norm1 comes with the tail
+        ta.g1n = W(layer + 1, 0);
+        ta.be1n = W(layer + 1, 1);
+        ta.ln_out = ln;
+        ln_ready = true;
+      }
+      e = enc::block_tail_bf16(ta, T, D, F, eps, cus, st);
+      if (e != hipSuccess) return fail_hip(e, "encoder block tail");
+      cur = ta.out;
+      continue;
+    }
+    // out_proj + residual; padded rows keep the residual (attention output is 0 there)
+    enc::GemmEpilogueArgs oa;
+    oa.bias = W(layer, 5);
+    oa.residual = cur;
+    oa.row_mask = row_mask;
+    oa.out = x_attn;
+    e = enc::gemm_bf16(ctx, W(layer, 4), T, D, D, enc::kEpiResidualKeep, oa, cus, st);
+    if (e != hipSuccess) return fail_hip(e, "encoder out_proj");
+    // norm2
+    e = enc::layernorm_bf16(x_attn, W(layer, 6), W(layer, 7), ln, T, D, eps, nullptr, st);
+    if (e != hipSuccess) return fail_hip(e, "encoder norm2");
+    // ffn_in + exact GELU
+    enc::GemmEpilogueArgs fa;
+    fa.bias = W(layer, 9);
+    fa.out = hidden;
+    e = enc::gemm_bf16(ln, W(layer, 8), T, F, D, enc::kEpiBiasGelu, fa, cus, st);
+    if (e != hipSuccess) return fail_hip(e, "encoder ffn_in");
+    // ffn_out + residual; padded rows are zeroed (block output masked_fill)
+    bf16_t* x_next = (!final_norm && layer == num_layers - 1) ? static_cast<bf16_t*>(out) : (x_attn == xa) ? xb : xa;
+    enc::GemmEpilogueArgs fo;
+    fo.bias = W(layer, 11);
+    fo.residual = x_attn;
+    fo.row_mask = row_mask;
+    fo.out = x_next;
+    e = enc::gemm_bf16(hidden, W(layer, 10), T, D, F, enc::kEpiResidualZero, fo, cus, st);
+    if (e != hipSuccess) return fail_hip(e, "encoder ffn_out");
+    cur = x_next;
+  }
+  if (!final_norm) return ok();  // out holds the last block's output
+  e = enc::layernorm_bf16(cur, static_cast<const bf16_t*>(weights[12 * num_layers]),
+                          static_cast<const bf16_t*>(weights[12 * num_layers + 1]), static_cast<bf16_t*>(out), T, D,
+                          eps, row_mask, st);
+  if (e != hipSuccess) return fail_hip(e, "encoder final_norm");
+  return ok();
+}
+
 
 }  // namespace
 
@@ -254,141 +439,39 @@ int enc_encoder_forward_bf16(const void* x, void* out, void* workspace, int64_t 
                              int64_t num_heads, int64_t ffn_dim, int64_t num_layers, float eps, int32_t causal,
                              const int32_t* kv_len, const uint8_t* key_mask, const uint8_t* row_mask,
                              int32_t flags, void* stream) {
-  if (flags & ~(ENC_FWD_ONLINE_ATTENTION | ENC_FWD_SKIP_FINAL_NORM))
-    return fail(ENC_ERR_INVALID, "encoder: unknown flags");
-  const bool final_norm = (flags & ENC_FWD_SKIP_FINAL_NORM) == 0;
-  if (!final_norm && num_layers < 1) return fail(ENC_ERR_INVALID, "encoder: skipping final_norm needs a layer");
-  const bool exact = (flags & ENC_FWD_ONLINE_ATTENTION) == 0;
-  int rc = check_encoder_shape(batch, seq_len, d_model, num_heads, ffn_dim, exact);
+  EncoderWorkspace w{};
+  int rc = check_encoder_call(x, out, weights, batch, seq_len, d_model, num_heads, ffn_dim, num_layers, eps, kv_len,
+                              key_mask, flags, &w);
   if (rc != ENC_OK) return rc;
-  if (num_layers < 0) return fail(ENC_ERR_INVALID, "encoder: num_layers must be >= 0");
-  if (!x || !out || !workspace || !weights) return fail(ENC_ERR_INVALID, "encoder: null pointer");
-  if (kv_len && key_mask) return fail(ENC_ERR_INVALID, "encoder: pass kv_len or key_mask, not both");
-  if (!(eps > 0.f)) return fail(ENC_ERR_INVALID, "encoder: eps must be positive");
-  const EncoderWorkspace w = plan_workspace(batch, seq_len, d_model, num_heads, ffn_dim);
+  if (!workspace) return fail(ENC_ERR_INVALID, "encoder: null workspace");
   if (workspace_bytes < w.total)
     return fail(ENC_ERR_INVALID, "encoder: workspace too small (" + std::to_string(workspace_bytes) + " < " +
                                      std::to_string(w.total) + ")");
-  for (int64_t i = 0; i < 12 * num_layers + 2; ++i)
-    if (!weights[i]) return fail(ENC_ERR_INVALID, "encoder: null weight pointer at index " + std::to_string(i));
+  return run_encoder_forward(x, out, workspace, w, weights, batch, seq_len, d_model, num_heads, ffn_dim, num_layers,
+                             eps, causal, kv_len, key_mask, row_mask, flags, stream);
+}
 
-  using enc::bf16_t;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  char* base = static_cast<char*>(workspace);
-  bf16_t* ln = reinterpret_cast<bf16_t*>(base + w.ln);
-  bf16_t* q = reinterpret_cast<bf16_t*>(base + w.q);
-  bf16_t* k = reinterpret_cast<bf16_t*>(base + w.k);
-  bf16_t* vt = reinterpret_cast<bf16_t*>(base + w.vt);
-  bf16_t* ctx = reinterpret_cast<bf16_t*>(base + w.ctx);
-  bf16_t* xa = reinterpret_cast<bf16_t*>(base + w.xa);
-  bf16_t* xb = reinterpret_cast<bf16_t*>(base + w.xb);
-  bf16_t* hidden = reinterpret_cast<bf16_t*>(base + w.hidden);
-
-  const int64_t T = batch * seq_len;
-  const int64_t D = d_model, F = ffn_dim, H = num_heads;
-  const int cus = device_cus();
-  const float scale = 1.0f / sqrtf(static_cast<float>(D / H));
-  auto W = [&](int64_t layer, int idx) { return static_cast<const bf16_t*>(weights[layer * 12 + idx]); };
-
-  // Narrow models with up to 8192 tokens run the block tail (out_proj ..
-  // ffn_out, and the next layer's norm1) as one kernel, whose 16-byte loads
-  // need 16-byte aligned weights (all but the QKV projection's).
-  // (With more tokens the four launches win: the fused kernel's one workgroup
-  // per CU cannot hide its per-slab latency; measured on MI355X.)
-  bool tail_fused = enc::block_tail_supported(D, F) && T <= 8192;
-  for (int64_t layer = 0; tail_fused && layer < num_layers; ++layer)
-    for (int idx = 0; idx < 12; ++idx)
-      tail_fused = tail_fused && (idx == 2 || idx == 3 || reinterpret_cast<uintptr_t>(W(layer, idx)) % 16 == 0);
-
-  const bf16_t* cur = static_cast<const bf16_t*>(x);
-  hipError_t e = hipSuccess;
-  bool ln_ready = false;  // the fused tail already wrote this layer's norm1
-  for (int64_t layer = 0; layer < num_layers; ++layer) {
-    bf16_t* x_attn = (cur == xa) ? xb : xa;  // residual stream after attention
-    // norm1
-    if (!ln_ready) {
-      e = enc::layernorm_bf16(cur, W(layer, 0), W(layer, 1), ln, T, D, eps, nullptr, st);
-      if (e != hipSuccess) return fail_hip(e, "encoder norm1");
-    }
-    ln_ready = false;
-    // packed QKV, head-major
-    enc::GemmEpilogueArgs qa;
-    qa.bias = W(layer, 3);
-    qa.q = q;
-    qa.k = k;
-    qa.v_t = vt;
-    qa.seq_len = static_cast<int>(seq_len);
-    qa.num_heads = static_cast<int>(H);
-    qa.head_dim = static_cast<int>(D / H);
-    qa.d_model = static_cast<int>(D);
-    qa.ld_vt = static_cast<int>(enc::vt_stride(seq_len));
-    e = enc::gemm_bf16(ln, W(layer, 2), T, 3 * D, D, enc::kEpiQkvHeadMajor, qa, cus, st);
-    if (e != hipSuccess) return fail_hip(e, "encoder qkv");
-    // attention -> context [T, D]
-    auto attention = exact ? enc::attention_fwd_bf16 : enc::flash_attention_fwd_bf16;
-    e = attention(q, k, vt, ctx, static_cast<int>(batch), static_cast<int>(H), static_cast<int>(seq_len),
-                  static_cast<int>(D / H), scale, causal != 0, kv_len, key_mask, st);
-    if (e != hipSuccess) return fail_hip(e, "encoder attention");
-    if (tail_fused) {
-      // out_proj .. ffn_out in one launch (narrow models), same arithmetic
-      enc::BlockTailArgs ta;
-      ta.ctx = ctx;
-      ta.x = cur;
-      ta.wo = W(layer, 4);
-      ta.bo = W(layer, 5);
-      ta.g2 = W(layer, 6);
-      ta.be2 = W(layer, 7);
-      ta.w1 = W(layer, 8);
-      ta.b1 = W(layer, 9);
-      ta.w2 = W(layer, 10);
-      ta.b2 = W(layer, 11);
-      ta.out = (!final_norm && layer == num_layers - 1) ? static_cast<bf16_t*>(out) : x_attn;
-      ta.row_mask = row_mask;
-      if (layer + 1 < num_layers) {  // the next layer's norm1 comes with the tail
-        ta.g1n = W(layer + 1, 0);
-        ta.be1n = W(layer + 1, 1);
-        ta.ln_out = ln;
-        ln_ready = true;
-      }
-      e = enc::block_tail_bf16(ta, T, D, F, eps, cus, st);
-      if (e != hipSuccess) return fail_hip(e, "encoder block tail");
-      cur = ta.out;
-      continue;
-    }
-    // out_proj + residual; padded rows keep the residual (attention output is 0 there)
-    enc::GemmEpilogueArgs oa;
-    oa.bias = W(layer, 5);
-    oa.residual = cur;
-    oa.row_mask = row_mask;
-    oa.out = x_attn;
-    e = enc::gemm_bf16(ctx, W(layer, 4), T, D, D, enc::kEpiResidualKeep, oa, cus, st);
-    if (e != hipSuccess) return fail_hip(e, "encoder out_proj");
-    // norm2
-    e = enc::layernorm_bf16(x_attn, W(layer, 6), W(layer, 7), ln, T, D, eps, nullptr, st);
-    if (e != hipSuccess) return fail_hip(e, "encoder norm2");
-    // ffn_in + exact GELU
-    enc::GemmEpilogueArgs fa;
-    fa.bias = W(layer, 9);
-    fa.out = hidden;
-    e = enc::gemm_bf16(ln, W(layer, 8), T, F, D, enc::kEpiBiasGelu, fa, cus, st);
-    if (e != hipSuccess) return fail_hip(e, "encoder ffn_in");
-    // ffn_out + residual; padded rows are zeroed (block output masked_fill)
-    bf16_t* x_next = (!final_norm && layer == num_layers - 1) ? static_cast<bf16_t*>(out) : (x_attn == xa) ? xb : xa;
-    enc::GemmEpilogueArgs fo;
-    fo.bias = W(layer, 11);
-    fo.residual = x_attn;
-    fo.row_mask = row_mask;
-    fo.out = x_next;
-    e = enc::gemm_bf16(hidden, W(layer, 10), T, D, F, enc::kEpiResidualZero, fo, cus, st);
-    if (e != hipSuccess) return fail_hip(e, "encoder ffn_out");
-    cur = x_next;
-  }
-  if (!final_norm) return ok();  // out holds the last block's output
-  e = enc::layernorm_bf16(cur, static_cast<const bf16_t*>(weights[12 * num_layers]),
-                          static_cast<const bf16_t*>(weights[12 * num_layers + 1]), static_cast<bf16_t*>(out), T, D,
-                          eps, row_mask, st);
-  if (e != hipSuccess) return fail_hip(e, "encoder final_norm");
-  return ok();
+int enc_encoder_forward_bf16_noalloc(const void* x, void* out, const void* const* weights, int64_t batch,
+                                     int64_t seq_len, int64_t d_model, int64_t num_heads, int64_t ffn_dim,
+                                     int64_t num_layers, float eps, int32_t causal, const int32_t* kv_len,
+                                     const uint8_t* key_mask, const uint8_t* row_mask, int32_t flags,
+                                     void* stream) {
+  EncoderWorkspace w{};
+  int rc = check_encoder_call(x, out, weights, batch, seq_len, d_model, num_heads, ffn_dim, num_layers, eps, kv_len,
+                              key_mask, flags, &w);
+  if (rc != ENC_OK) return rc;
+  if (w.total > kScratchBytes)
+    return fail(ENC_ERR_UNSUPPORTED, "encoder noalloc: this shape needs " + std::to_string(w.total) +
+                                         " bytes of workspace, above the library's " +
+                                         std::to_string(kScratchBytes) + "-byte scratch array");
+  void* ws = nullptr;
+  rc = scratch_for_current_device(&ws);
+  if (rc != ENC_OK) return rc;
+  // Every buffer of the workspace is written by a kernel of the forward before
+  // any kernel reads it, so the array's contents from an earlier call need no
+  // clearing.
+  return run_encoder_forward(x, out, ws, w, weights, batch, seq_len, d_model, num_heads, ffn_dim, num_layers, eps,
+                             causal, kv_len, key_mask, row_mask, flags, stream);
 }
 
 }  // extern "C"

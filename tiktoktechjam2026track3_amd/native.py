@@ -64,7 +64,15 @@ SIGNATURES = (
         ctypes.c_int,
         (_VP, _VP, _VP, _I64, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _F32, _I32, _VP, _VP, _VP, _I32, _VP),
     ),
+    (
+        "enc_encoder_forward_bf16_noalloc",
+        ctypes.c_int,
+        (_VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _F32, _I32, _VP, _VP, _VP, _I32, _VP),
+    ),
 )
+
+# Bytes of the library's static scratch array (ENC_NOALLOC_SCRATCH_BYTES).
+NOALLOC_SCRATCH_BYTES = 64 * 1024 * 1024
 
 
 class NativeLibraryError(RuntimeError):
@@ -334,6 +342,39 @@ def encoder_forward(
         "enc_encoder_forward_bf16",
         load_library().enc_encoder_forward_bf16(
             x.data_ptr(), out.data_ptr(), workspace.data_ptr(), workspace.numel(), table.value,
+            batch, seq_len, d_model, num_heads, ffn_dim, num_layers, float(eps), int(bool(causal)),
+            _ptr(kv_len), _ptr(key_mask), _ptr(row_mask),
+            flags, _stream(x.device),
+        ),
+    )
+
+
+def encoder_forward_noalloc(
+    x: torch.Tensor,
+    out: torch.Tensor,
+    weight_table: torch.Tensor,
+    num_heads: int,
+    ffn_dim: int,
+    num_layers: int,
+    eps: float,
+    causal: bool,
+    kv_len: Optional[torch.Tensor],
+    key_mask: Optional[torch.Tensor],
+    row_mask: Optional[torch.Tensor],
+    online_attention: bool = False,
+    final_norm: bool = True,
+) -> None:
+    """enc_encoder_forward_bf16_noalloc: the encoder forward over the library's
+    own static scratch array (no workspace argument, no device allocation).
+    Calls that overlap on one GPU share that array and must not run
+    concurrently."""
+    flags = (ENC_FWD_ONLINE_ATTENTION if online_attention else 0) | (0 if final_norm else ENC_FWD_SKIP_FINAL_NORM)
+    batch, seq_len, d_model = x.shape
+    table = ctypes.cast(weight_table.data_ptr(), ctypes.c_void_p)
+    _check(
+        "enc_encoder_forward_bf16_noalloc",
+        load_library().enc_encoder_forward_bf16_noalloc(
+            x.data_ptr(), out.data_ptr(), table.value,
             batch, seq_len, d_model, num_heads, ffn_dim, num_layers, float(eps), int(bool(causal)),
             _ptr(kv_len), _ptr(key_mask), _ptr(row_mask),
             flags, _stream(x.device),
