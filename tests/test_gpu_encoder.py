@@ -115,46 +115,59 @@ def test_encoder_parity_second_trial_c4(device):
     assert result["passed"], result
 
 
-@pytest.mark.slow
-def test_encoder_parity_c5_sampled_sequences(device):
-    """c5 (B=32, S=100000): the whole batch runs through the HIP forward; the
-    oracle recomputes sampled sequences over all layers, with its Linear
-    layers on the whole [3.2M, 1024] batch as the reference runs them and its
-    attention walking equal 1000-row query blocks (scores are never
-    materialised for more rows than that).
+# Sampled c5 sequences: the first, a middle one, two whose element offsets pass
+# 2^31 (activations and head-major Q/K beyond sequence 20), and the last, whose
+# final ~18K rows are the library's stream-K tail tiles.
+C5_SEQUENCES = (0, 16, 24, 30, 31)
 
-    The first and a middle sequence must pass the strict gate (they come out
-    bit-identical).  The last sequence's final ~18K rows fall in the tail
-    tiles that hipBLASLt's Stream-K kernel for this [3.2M, 1024] x [1024, N]
-    shape splits along K; the HIP GEMM accumulates those tiles in one pass, so
-    about 2^-16 of their outputs differ in the last bf16 bit, which the
-    attention over 100000 keys spreads.  That sequence is held to the
-    allclose form of the gate and to a failure fraction below 1e-5."""
+
+def _c5_sampled(device, causal: bool):
     spec = ENCODER_CONFIGS["c5"]
     cfg = spec.config
     sd, candidate = build_models(cfg, spec.seed, device)
-    seqs = (0, cfg.batch_size // 2, cfg.batch_size - 1)
+    candidate.config = TransformerConfig(cfg.batch_size, cfg.seq_len, cfg.d_model, cfg.num_heads, cfg.ffn_dim,
+                                         cfg.num_layers, causal)
+    name = "case 14 (causal c5)" if causal else "c5"
     with torch.inference_mode():
         x, mask = generate_random_case(cfg, device, torch.bfloat16, spec.seed, spec.padding_ratio, 1.0)
         out = candidate(x, mask)
         torch.cuda.synchronize()
-        print(f"[c5] candidate forward done, finite={bool(torch.isfinite(out).all())}", flush=True)
-        picked = out[list(seqs)].clone()
+        print(f"[{name}] candidate forward done, finite={bool(torch.isfinite(out).all())}", flush=True)
+        picked = out[list(C5_SEQUENCES)].clone()
         del out
         candidate._hip.workspace = None  # room for the oracle's full-batch activations
         torch.cuda.empty_cache()
-        ref = encoder_forward_sequences(sd, x, seqs, cfg.causal, cfg.num_heads, cfg.num_layers)
+        ref = encoder_forward_sequences(sd, x, C5_SEQUENCES, causal, cfg.num_heads, cfg.num_layers)
     results = []
-    for i, b in enumerate(seqs):
+    for i, b in enumerate(C5_SEQUENCES):
         result = compare(ref[i], picked[i], RTOL, ATOL)
         bitwise = float((ref[i].view(torch.int16) == picked[i].view(torch.int16)).float().mean())
-        print(f"[parity] c5 sequence {b}: {result} bitwise={bitwise:.6f}", flush=True)
-        results.append(result)
-    for result in results[:-1]:
-        assert result["passed"], result
-    last = results[-1]
-    assert last["allclose"], last
-    assert last["failed"] < 1e-5 * last["total"], last
+        results.append((b, result, bitwise))
+    for b, result, bitwise in results:  # one verdict line per sequence, at the end
+        print(f"[parity] {name} sequence {b}: passed={result['passed']} failed={result['failed']}/"
+              f"{result['total']} max_abs_error={result['max_abs_error']} bitwise={bitwise:.6f}", flush=True)
+    return results
+
+
+@pytest.mark.slow
+def test_encoder_parity_c5_sampled_sequences(device):
+    """c5 (B=32, S=100000): the whole batch runs through the HIP forward; the
+    oracle recomputes the sampled sequences over all layers, with its Linear
+    layers on the whole [3.2M, 1024] batch as the reference runs them and its
+    attention walking equal 1000-row query blocks (scores are never
+    materialised for more rows than that).  Every sampled sequence is held to
+    the strict gate."""
+    for b, result, _ in _c5_sampled(device, causal=False):
+        assert result["passed"], (b, result)
+
+
+@pytest.mark.slow
+def test_encoder_parity_case14_causal_c5_sampled_sequences(device):
+    """The reference's official case 14 (cases.py:56): c5's shape with a causal
+    mask, which ran out of memory on the reference's GPU.  Same sampling and
+    strict gate as c5."""
+    for b, result, _ in _c5_sampled(device, causal=True):
+        assert result["passed"], (b, result)
 
 
 def test_graph_replay_matches_eager(device):

@@ -212,6 +212,36 @@ def test_linear_split_k_order_bitwise(device, m, n, k):
     assert torch.equal(out_res, res + F.linear(a, w, bias))
 
 
+@pytest.mark.parametrize("m", [3200000, 100000])
+def test_linear_streamk_tail_bitwise(device, m):
+    """[M, 1024] x [1024, 1024]^T at c5's M (and one sequence's): the library
+    accumulates its last ~18K rows as stream-K tiles whose K range is split in
+    two partial sums (csrc/streamk_tail.h); the kernel reproduces the split, so
+    every output, tail rows included, is equal bit for bit.  The packed QKV
+    projection matches the three separate products the reference runs."""
+    g = torch.Generator(device=device).manual_seed(m % 9973)
+    a = torch.randn(m, 1024, generator=g, device=device).bfloat16()
+    w = ((torch.rand(1024, 1024, generator=g, device=device) * 2 - 1) / 32).bfloat16()
+    bias = ((torch.rand(1024, generator=g, device=device) * 2 - 1) / 32).bfloat16()
+    ref = F.linear(a, w, bias)
+    out = native.linear(a, w, bias, native.ENC_EPI_BIAS)
+    mismatches = int((ref.view(torch.int16) != out.view(torch.int16)).sum())
+    print(f"[streamk] M={m}: {mismatches} mismatching outputs", flush=True)
+    assert mismatches == 0
+    assert torch.equal(native.linear(a, w, bias, native.ENC_EPI_BIAS_GELU), F.gelu(ref, approximate="none"))
+    del out
+    if m == 3200000:
+        w3 = ((torch.rand(3072, 1024, generator=g, device=device) * 2 - 1) / 32).bfloat16()
+        b3 = ((torch.rand(3072, generator=g, device=device) * 2 - 1) / 32).bfloat16()
+        q, k, v_t = native.qkv_proj(a.view(32, 100000, 1024), w3, b3, 16)
+        for i, got in enumerate((q, k)):
+            part = F.linear(a, w3[1024 * i:1024 * (i + 1)], b3[1024 * i:1024 * (i + 1)])
+            assert torch.equal(part.view(32, 100000, 16, 64).transpose(1, 2), got)
+            del part
+        part = F.linear(a, w3[2048:], b3[2048:])
+        assert torch.equal(part.view(32, 100000, 16, 64).permute(0, 2, 3, 1), v_t[..., :100000])
+
+
 @pytest.mark.parametrize(
     "b,s,d,h",
     [(1, 128, 512, 8), (2, 100, 512, 8), (8, 1024, 1024, 16), (3, 37, 1024, 16), (64, 128, 32, 4), (3, 37, 128, 16),

@@ -24,6 +24,7 @@
 // rows so concurrently running tiles share A rows and W columns in that XCD's L2.
 #include "common.h"
 #include "kernels.h"
+#include "streamk_tail.h"
 
 namespace enc {
 
@@ -1008,6 +1009,180 @@ hipError_t launch_big(const bf16_t* A, const bf16_t* W, int M, int N, int K, int
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Stream-K tail.  For the shapes in streamk_tail.h the library accumulates its
+// last 256 x 256 output tiles in two partial sums, K < s and K >= s (s per
+// tile, measured), and adds them before the bias.  This kernel computes those
+// rows the same way: 128 x 128 workgroup tiles (each inside one library tile),
+// sequential 16-deep MFMA steps inside each partial, then
+//   y = bf16((P1 + P2) + bias)          (s > 0)
+//   y = bf16(P + bias)                  (s == 0: one pass, as elsewhere)
+// through the usual epilogue.  Only the tail rows run here (0.6% of c5's rows),
+// so the kernel stages operands through registers and LDS plainly.
+constexpr int kTailMaxTiles = 288;
+struct TailSplitArgs {
+  int row_begin;   // first row of the tail, a multiple of 256
+  int slice_n;     // N of the library product the table describes
+  int tile_cols;   // 256-wide tiles per slice
+  uint16_t split[kTailMaxTiles];
+};
+
+template <int EPI>
+__global__ void __launch_bounds__(kThreads)
+gemm_tail_split_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int M, int N, int K,
+                       TailSplitArgs ts, GemmEpilogueArgs ep) {
+  constexpr int BM = 128, BN = 128, RM = 2, RN = 2;
+  constexpr int A_LOADS = BM * (kBK / 8) / kThreads;
+  constexpr int B_LOADS = BN * (kBK / 8) / kThreads;
+  __shared__ __attribute__((aligned(16))) bf16_t sA[2][BM * kLdk];
+  __shared__ __attribute__((aligned(16))) bf16_t sB[2][BN * kLdk];
+
+  const int tiles_n = N / BN;
+  const int tm = blockIdx.x / tiles_n;
+  const int tn = blockIdx.x - tm * tiles_n;
+  const int m0 = ts.row_begin + tm * BM;
+  const int n0 = tn * BN;
+  const int lib_row = (m0 - ts.row_begin) / 256;
+  const int lib_col = (n0 % ts.slice_n) / 256;
+  const int split = ts.split[lib_row * ts.tile_cols + lib_col];
+
+  const int tid = threadIdx.x;
+  const int lane = tid % kWave;
+  const int wave = tid / kWave;
+  const int wm = wave >> 1;
+  const int wn = wave & 1;
+  const int l32 = lane & 31;
+  const int lhi = lane >> 5;
+
+  u32x4 ra[A_LOADS];
+  u32x4 rb[B_LOADS];
+  auto load_global = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < A_LOADS; ++i) {
+      const int c = tid + i * kThreads;
+      const int grow = min(m0 + (c >> 3), M - 1);  // rows past M are never stored
+      ra[i] = *reinterpret_cast<const u32x4*>(A + static_cast<int64_t>(grow) * K + k0 + (c & 7) * 8);
+    }
+#pragma unroll
+    for (int i = 0; i < B_LOADS; ++i) {
+      const int c = tid + i * kThreads;
+      rb[i] = *reinterpret_cast<const u32x4*>(W + static_cast<int64_t>(n0 + (c >> 3)) * K + k0 + (c & 7) * 8);
+    }
+  };
+  auto store_lds = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < A_LOADS; ++i) {
+      const int c = tid + i * kThreads;
+      *reinterpret_cast<u32x4*>(&sA[buf][(c >> 3) * kLdk + (c & 7) * 8]) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < B_LOADS; ++i) {
+      const int c = tid + i * kThreads;
+      *reinterpret_cast<u32x4*>(&sB[buf][(c >> 3) * kLdk + (c & 7) * 8]) = rb[i];
+    }
+  };
+
+  f32x16 p1[RM][RN], p2[RM][RN];
+#pragma unroll
+  for (int i = 0; i < RM; ++i)
+#pragma unroll
+    for (int j = 0; j < RN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        p1[i][j][r] = 0.f;
+        p2[i][j][r] = 0.f;
+      }
+
+  const int KT = K / kBK;
+  load_global(0);
+  store_lds(0);
+  __syncthreads();
+  const int a_base = (wm * (BM / 2) + l32) * kLdk + lhi * 8;
+  const int b_base = (wn * (BN / 2) + l32) * kLdk + lhi * 8;
+  for (int kt = 0; kt < KT; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < KT) load_global((kt + 1) * kBK);
+    const bool second = kt * kBK >= split;  // uniform: which partial this K block feeds
+#pragma unroll
+    for (int ks = 0; ks < kBK / 16; ++ks) {
+      bf16x8 af[RM], bfr[RN];
+#pragma unroll
+      for (int i = 0; i < RM; ++i)
+        af[i] = *reinterpret_cast<const bf16x8*>(&sA[cur][a_base + i * 32 * kLdk + ks * 16]);
+#pragma unroll
+      for (int j = 0; j < RN; ++j)
+        bfr[j] = *reinterpret_cast<const bf16x8*>(&sB[cur][b_base + j * 32 * kLdk + ks * 16]);
+      if (second) {
+#pragma unroll
+        for (int i = 0; i < RM; ++i)
+#pragma unroll
+          for (int j = 0; j < RN; ++j)
+            p2[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], p2[i][j], 0, 0, 0);
+      } else {
+#pragma unroll
+        for (int i = 0; i < RM; ++i)
+#pragma unroll
+          for (int j = 0; j < RN; ++j)
+            p1[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], p1[i][j], 0, 0, 0);
+      }
+    }
+    if (kt + 1 < KT) store_lds(cur ^ 1);
+    __syncthreads();
+  }
+
+  const int row_base = m0 + wm * (BM / 2);
+  const int col_base = n0 + wn * (BN / 2);
+#pragma unroll
+  for (int j = 0; j < RN; ++j) {
+    const int col = col_base + j * 32 + l32;
+    const float bias = bf16_to_f32(ep.bias[col]);
+#pragma unroll
+    for (int i = 0; i < RM; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = row_base + i * 32 + 8 * (r >> 2) + 4 * lhi + (r & 3);
+        if (row >= M) continue;
+        // (P1 + P2) + bias, matched bitwise against the library on random
+        // inputs; the other orders, P1 + (P2 + bias) and (P1 + bias) + P2,
+        // were measured to differ.  With no split every K block went to p2.
+        const float sum = split == 0 ? p2[i][j][r] : p1[i][j][r] + p2[i][j][r];
+        store_one<EPI>(ep, N, row, col, sum, bias);
+      }
+    }
+  }
+}
+
+// The stream-K tail table for this product, or null.  The packed QKV
+// projection (N = 3 x slice_n, head-major epilogue) matches too: the reference
+// runs the q, k and v projections as three [M, K] x [slice_n, K]^T products.
+const StreamKTail* find_streamk_tail(int64_t M, int64_t N, int64_t K, int epi) {
+  for (const StreamKTail& t : kStreamKTails)
+    if (t.m == M && t.k == K && (N == t.n || (epi == kEpiQkvHeadMajor && N == 3 * t.n))) return &t;
+  return nullptr;
+}
+
+hipError_t launch_tail_split(const bf16_t* A, const bf16_t* W, int M, int N, int K, int epi,
+                             const StreamKTail& t, const GemmEpilogueArgs& ep, hipStream_t st) {
+  TailSplitArgs ts;
+  ts.row_begin = t.first_tile_row * 256;
+  ts.slice_n = t.n;
+  ts.tile_cols = t.tile_cols;
+  const int entries = t.tile_rows * t.tile_cols;
+  if (entries > kTailMaxTiles) return hipErrorInvalidValue;
+  for (int i = 0; i < kTailMaxTiles; ++i) ts.split[i] = i < entries ? t.split[i] : 0;
+  const int rows = M - ts.row_begin;
+  const dim3 grid(static_cast<uint32_t>((rows + 127) / 128 * (N / 128))), block(kThreads);
+  switch (epi) {
+    case kEpiBias: hipLaunchKernelGGL(gemm_tail_split_kernel<kEpiBias>, grid, block, 0, st, A, W, M, N, K, ts, ep); break;
+    case kEpiBiasGelu: hipLaunchKernelGGL(gemm_tail_split_kernel<kEpiBiasGelu>, grid, block, 0, st, A, W, M, N, K, ts, ep); break;
+    case kEpiResidualKeep: hipLaunchKernelGGL(gemm_tail_split_kernel<kEpiResidualKeep>, grid, block, 0, st, A, W, M, N, K, ts, ep); break;
+    case kEpiResidualZero: hipLaunchKernelGGL(gemm_tail_split_kernel<kEpiResidualZero>, grid, block, 0, st, A, W, M, N, K, ts, ep); break;
+    case kEpiQkvHeadMajor: hipLaunchKernelGGL(gemm_tail_split_kernel<kEpiQkvHeadMajor>, grid, block, 0, st, A, W, M, N, K, ts, ep); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 // Tile of the large-tile kernel for this shape, or 0 when the small-tile
 // kernel should run: the operands must be 16-byte aligned (16-byte loads per
 // lane), the residual / outputs too (16-byte epilogue stores), and the tile
@@ -1092,8 +1267,12 @@ bool gemm_supported(int64_t M, int64_t N, int64_t K) {
          N < (int64_t(1) << 20) && K < (int64_t(1) << 20);
 }
 
-hipError_t gemm_bf16(const bf16_t* A, const bf16_t* W, int64_t M, int64_t N, int64_t K, int epi,
-                     const GemmEpilogueArgs& ep, int num_cus, hipStream_t stream) {
+namespace {
+
+// The product without the stream-K tail rule: every tile in one pass (or the
+// small-M split plan).
+hipError_t gemm_bf16_plain(const bf16_t* A, const bf16_t* W, int64_t M, int64_t N, int64_t K, int epi,
+                           const GemmEpilogueArgs& ep, int num_cus, hipStream_t stream) {
   if (M == 0) return hipSuccess;
   const int m = static_cast<int>(M), n = static_cast<int>(N), k = static_cast<int>(K);
   // N or K not a multiple of 64: one 32x32 block per wavefront, sequential K
@@ -1136,6 +1315,19 @@ hipError_t gemm_bf16(const bf16_t* A, const bf16_t* W, int64_t M, int64_t N, int
   if (bm == 128 && bn == 128) return launch_tile<128, 128>(A, W, m, n, k, epi, ep, stream);
   if (bm == 128 && bn == 64) return launch_tile<128, 64>(A, W, m, n, k, epi, ep, stream);
   return launch_tile<64, 64>(A, W, m, n, k, epi, ep, stream);
+}
+
+}  // namespace
+
+hipError_t gemm_bf16(const bf16_t* A, const bf16_t* W, int64_t M, int64_t N, int64_t K, int epi,
+                     const GemmEpilogueArgs& ep, int num_cus, hipStream_t stream) {
+  const StreamKTail* tail = find_streamk_tail(M, N, K, epi);
+  if (tail == nullptr) return gemm_bf16_plain(A, W, M, N, K, epi, ep, num_cus, stream);
+  // rows before the library's stream-K tail as usual, the tail's rows split
+  const int64_t row_begin = static_cast<int64_t>(tail->first_tile_row) * 256;
+  hipError_t e = gemm_bf16_plain(A, W, row_begin, N, K, epi, ep, num_cus, stream);
+  if (e != hipSuccess) return e;
+  return launch_tail_split(A, W, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), epi, *tail, ep, stream);
 }
 
 }  // namespace enc
