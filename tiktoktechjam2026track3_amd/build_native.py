@@ -76,6 +76,9 @@ def _hipcc() -> str:
 
 def _run(cmd: list[str]) -> None:
     proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    # hipcc's host pass does not know the device feature; whether the device
+    # pass applied it is checked on the built code (no packed FP32 instructions,
+    # _check_mfma_hazards)
     noise = "is not a recognized feature for this target"
     output = "\n".join(
         line for line in proc.stdout.splitlines() if noise not in line
@@ -112,8 +115,27 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
         print(" ".join(link))
     _run(link)
     _check_launch_stubs(tmp)
+    _check_mfma_hazards(objects, jobs=workers)
     os.replace(tmp, LIBRARY_PATH)
     return LIBRARY_PATH
+
+
+def _check_mfma_hazards(objects, jobs: int) -> None:
+    """Fail the build when any path reads an MFMA result too early, or when
+    packed FP32 instructions appear (hazard_check.py: the device code is
+    disassembled and every path after each MFMA is walked)."""
+    from . import hazard_check
+
+    if not hazard_check.tools_available():
+        print("warning: ROCm LLVM tools not found; MFMA hazard check skipped", file=sys.stderr)
+        return
+    report = hazard_check.check_objects(objects, jobs=jobs)
+    if report.findings:
+        details = "\n".join(str(f) for f in report.findings[:20])
+        raise RuntimeError(f"MFMA result read with too few wait states ({len(report.findings)} finding(s)):\n{details}")
+    if report.packed_fp32:
+        details = "\n".join(report.packed_fp32[:20])
+        raise RuntimeError(f"packed FP32 instructions in the device code (-packed-fp32-ops not honoured):\n{details}")
 
 
 def _check_launch_stubs(path: Path) -> None:

@@ -312,6 +312,8 @@ hipError_t block_tail_bf16(const BlockTailArgs& a, int64_t rows, int64_t d_model
                            int num_cus, hipStream_t stream) {
   if (rows == 0) return hipSuccess;
   if (!block_tail_supported(d_model, ffn_dim) || rows >= (int64_t(1) << 31)) return hipErrorInvalidValue;
+  // the kernel reads x and writes out through restrict pointers
+  if (a.out == a.x || (a.ln_out != nullptr && (a.ln_out == a.x || a.ln_out == a.out))) return hipErrorInvalidValue;
   const int r = static_cast<int>(rows);
   switch (d_model) {
     case 32: return launch_tail_f<32>(static_cast<int>(ffn_dim), a, r, eps, num_cus, stream);

@@ -96,7 +96,7 @@ struct BlockTailArgs {
   const bf16_t* b1 = nullptr;
   const bf16_t* w2 = nullptr;   // ffn_out weight [D, F] and bias [D]
   const bf16_t* b2 = nullptr;
-  bf16_t* out = nullptr;        // block output [T, D]; may alias x
+  bf16_t* out = nullptr;        // block output [T, D]; must not alias x (rejected)
   const uint8_t* row_mask = nullptr;
   // optional: the next layer's norm1 (weight, bias) applied to the block
   // output, written to ln_out [T, D] (no row mask, as the separate launch)
