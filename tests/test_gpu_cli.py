@@ -71,3 +71,24 @@ def test_cli_remaining_official_cases_1_to_13_pass(tmp_path):
     for case in doc["cases"]:
         assert case["status"] == "succeeded"
         assert case["accuracy"]["failed_elements"] == 0
+
+
+def test_cli_encoder_config_c1_on_the_gpu_box(tmp_path):
+    """c1 (B=2, S=128, D=256, H=4, FFN=1024, L=2, fp32, seed 0) is the
+    reference's CPU smoke case: on the GPU box the CLI still runs it through
+    the candidate's CPU path (the reference's CPU fallback contract) and holds
+    it to the reference gate against the baseline, bit for bit."""
+    out = tmp_path / "c1.json"
+    cmd = [sys.executable, "-u", str(ROOT / "torch_transformer_benchmark.py"), "--encoder-configs", "c1",
+           "--rtol", "1.6e-2", "--atol", "1e-2", "--accuracy-trials", "2", "--warmup", "1", "--repeats", "3",
+           "--benchmark-rounds", "1", "--json-output", str(out)]
+    proc = subprocess.run(cmd, cwd=ROOT, capture_output=True, text=True, timeout=600)
+    print(proc.stdout[-3000:], proc.stderr[-2000:], flush=True)
+    assert proc.returncode == 0
+    doc = json.loads(out.read_text())
+    assert benchmarkctl_summary(doc) == {"mode": "official_matrix", "correctness_passed": True}
+    (case,) = doc["cases"]
+    assert case["status"] == "succeeded"
+    assert case["accuracy"]["failed_elements"] == 0 and case["accuracy"]["max_abs_error"] == 0.0
+    assert case["config"]["d_model"] == 256 and case["config"]["num_layers"] == 2
+    print(f"[c1] {json.dumps(case['accuracy'])}", flush=True)
