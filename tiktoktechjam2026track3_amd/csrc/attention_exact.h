@@ -74,15 +74,29 @@ enum MaskMode : int { kMaskNone = 0, kMaskPrefix = 1, kMaskBytes = 2 };
 // LDS tiles, in 16-byte chunks of 8 bf16:
 //   K tile:   64 keys x HD channels, HD / 8 chunks per row;
 //   V^T tile: HD channels x 64 keys, 8 chunks per row.
-// Chunk c of row r sits in slot c ^ (r & m), m = min(chunks per row, 8) - 1,
-// so the rows one MFMA fragment read touches at a fixed chunk spread over
-// distinct bank groups.
+// Chunk c of row r sits in slot c ^ swz(r), so the rows one MFMA fragment
+// read touches at a fixed chunk spread over distinct bank groups.  A 16-byte
+// read serves 16 lanes per LDS cycle, here 16 consecutive rows (in K's
+// permuted row order, still rows 16k .. 16k+15); with 128-byte rows (8
+// chunks: K at head dim 64, every V^T tile) the row's parity picks the bank
+// half and swz(r) = (r >> 1) & 7 the 16-byte group inside it, so those 16
+// rows hit 16 distinct groups (r & 7 would pair rows r and r + 8).  Other
+// head dims keep c ^ (r & m), m = min(chunks per row, 8) - 1.
+template <int HD>
+__device__ __forceinline__ int k_swz(int row) {
+  constexpr int kSwz = (HD / 8 < 8 ? HD / 8 : 8) - 1;
+  if constexpr (HD == 64) {
+    return (row >> 1) & 7;
+  } else {
+    return row & kSwz;
+  }
+}
 template <int HD>
 __device__ __forceinline__ int k_off(int row, int chunk) {
-  constexpr int kSwz = (HD / 8 < 8 ? HD / 8 : 8) - 1;
-  return row * HD + ((chunk ^ (row & kSwz)) << 3);
+  return row * HD + ((chunk ^ k_swz<HD>(row)) << 3);
 }
-__device__ __forceinline__ int v_off(int row, int chunk) { return row * kBKV + ((chunk ^ (row & 7)) << 3); }
+__device__ __forceinline__ int v_swz(int row) { return (row >> 1) & 7; }
+__device__ __forceinline__ int v_off(int row, int chunk) { return row * kBKV + ((chunk ^ v_swz(row)) << 3); }
 
 // s_waitcnt immediate: wait until no vector-memory operation is outstanding
 // (expcnt and lgkmcnt left at their no-wait maxima; gfx9 encoding).
@@ -232,12 +246,12 @@ attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
       if (kSlabs % NW != 0 && slab >= kSlabs) break;  // uniform per wavefront
       const int rk0 = (kWave / kChunksK) * slab;
       const int rk = rk0 + lane / kChunksK;
-      const int ck = (lane % kChunksK) ^ (rk & ((kChunksK < 8 ? kChunksK : 8) - 1));
+      const int ck = (lane % kChunksK) ^ k_swz<HD>(rk);
       __builtin_amdgcn_global_load_lds(Kh + static_cast<int64_t>(k0 + rk) * HD + ck * 8,
                                        &sK[buf * kTileElems + rk0 * HD], 16, 0, 0);
       if (with_v) {
         const int rv0 = 8 * slab;
-        const int cv = (lane & 7) ^ (lane >> 3);
+        const int cv = (lane & 7) ^ v_swz(rv0 + (lane >> 3));
         __builtin_amdgcn_global_load_lds(Vh + static_cast<int64_t>(rv0 + (lane >> 3)) * ld_vt + k0 + cv * 8,
                                          &sV[buf * kTileElems + rv0 * kBKV], 16, 0, 0);
       }
