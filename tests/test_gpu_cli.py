@@ -92,3 +92,35 @@ def test_cli_encoder_config_c1_on_the_gpu_box(tmp_path):
     assert case["accuracy"]["failed_elements"] == 0 and case["accuracy"]["max_abs_error"] == 0.0
     assert case["config"]["d_model"] == 256 and case["config"]["num_layers"] == 2
     print(f"[c1] {json.dumps(case['accuracy'])}", flush=True)
+
+
+def test_cli_profile_candidate_with_rocprof_evidence(tmp_path):
+    """--profile-candidate --rocprof on c2 and c3: rocprofv3 child processes
+    (kernel trace, FETCH_SIZE, WRITE_SIZE, MFMA busy) replay the focused cases
+    before the CLI touches the GPU; each case's profile then carries per-kernel
+    time, HBM bytes and GB/s and MFMA utilisation of the HIP kernels."""
+    out = tmp_path / "result.json"
+    cmd = [sys.executable, "-u", str(ROOT / "torch_transformer_benchmark.py"), "--encoder-configs", "c2", "c3",
+           "--rtol", "1.6e-2", "--atol", "1e-2", "--accuracy-trials", "1", "--warmup", "2", "--repeats", "5",
+           "--benchmark-rounds", "1", "--profile-candidate", "--rocprof", "--rocprof-dir", str(tmp_path / "prof"),
+           "--rocprof-timeout", "240", "--json-output", str(out)]
+    proc = subprocess.run(cmd, cwd=ROOT, capture_output=True, text=True, timeout=900)
+    print(proc.stdout[-3000:], proc.stderr[-2000:], flush=True)
+    assert proc.returncode == 0
+    doc = json.loads(out.read_text())
+    assert benchmarkctl_summary(doc) == {"mode": "official_matrix", "correctness_passed": True}
+    for case in doc["cases"]:
+        roc = case["candidate_profile"]["rocprof"]
+        names = [k["kernel"] for k in roc["kernels"]]
+        print(case["case_id"], [(k["name"][:40], k["calls"], round(k["avg_us"], 2), k["mfma_busy"],
+                                 k["hbm_gbps"]) for k in roc["kernels"][:6]], flush=True)
+        assert any("attn_fwd_kernel" in n for n in names)
+        assert any("gemm" in n for n in names)
+        assert not any("spin_kernel" in n or "copyBuffer" in n for n in names)
+        assert 0 < roc["calibration"]["fetch_bytes_per_unit"] and 0 < roc["calibration"]["write_bytes_per_unit"]
+        layers = case["config"]["num_layers"]
+        attn = next(k for k in roc["kernels"] if "attn_fwd_kernel" in k["kernel"])
+        assert attn["calls"] == 3 * layers  # three profiled forwards, one attention launch per layer
+        gemm = max((k for k in roc["kernels"] if "gemm" in k["kernel"]), key=lambda k: k["total_ms"])
+        assert 0 < gemm["mfma_busy"] <= 1
+        assert gemm["hbm_gbps"] > 0 and gemm["fetched_bytes_per_call"] > 0

@@ -23,7 +23,12 @@ validates:
     figure; a sequence too long for the host is reported as not run, with
     the reason;
   * a shape the HIP kernels do not cover is a case result with status
-    ``execution_failed`` and failure category ``unsupported_shape``.
+    ``execution_failed`` and failure category ``unsupported_shape``;
+  * ``--profile-candidate --rocprof`` adds rocprofv3 evidence per kernel
+    (time, HBM bytes and GB/s, MFMA utilisation) to each focused case's
+    bounded profile, under ``candidate_profile.rocprof``; the profiled
+    program runs as child processes started before this process touches the
+    GPU (``--rocprof-child`` is their mode).
 """
 
 from __future__ import annotations
@@ -34,6 +39,8 @@ import json
 import math
 import os
 import platform
+import sys
+import tempfile
 import time
 from dataclasses import asdict
 from pathlib import Path
@@ -50,9 +57,14 @@ from .profiling import (
     PROFILE_MAX_CASES,
     PROFILE_MAX_EVENTS,
     PROFILE_WARMUP_REPLAYS,
+    ROCPROF_PASSES,
+    calibration_copy,
     profile_candidate,
+    region_marker,
+    run_rocprof_passes,
+    summarize_rocprof,
 )
-from .timing import benchmark_models
+from .timing import benchmark_models, warmup_model
 
 MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
 ENCODER_CONFIG_NAMES = tuple(sorted(ENCODER_CONFIGS))
@@ -115,6 +127,14 @@ def parse_args(argv: Optional[Sequence[str]] = None) -> argparse.Namespace:
     parser.add_argument("--profile-candidate", action="store_true",
                         help="after correctness and timing, collect a bounded candidate-only profile "
                              "for an explicit focused case list")
+    parser.add_argument("--rocprof", action="store_true",
+                        help="with --profile-candidate, also collect rocprofv3 kernel time, HBM traffic and "
+                             "MFMA utilisation per kernel (child processes, one per counter pass)")
+    parser.add_argument("--rocprof-dir", type=Path,
+                        help="directory for the rocprofv3 runs (default: a new temporary directory)")
+    parser.add_argument("--rocprof-timeout", type=float, default=900.0,
+                        help="seconds each rocprofv3 pass may take")
+    parser.add_argument("--rocprof-child", action="store_true", help=argparse.SUPPRESS)
     parser.add_argument("--compile-baseline", action="store_true")
     parser.add_argument("--compile-user", action="store_true")
     parser.add_argument("--compile-mode", choices=("default", "reduce-overhead", "max-autotune"), default="default")
@@ -154,12 +174,8 @@ def validate_args(args: argparse.Namespace, device: torch.device, dtype: torch.d
             "the full official matrix requires a GPU; use --official-cases for a "
             "CPU subset or --no-official-matrix for a custom CPU smoke test"
         )
+    validate_profile_focus(args)
     if args.profile_candidate:
-        focused = args.encoder_configs or (args.official_cases if args.official_matrix else None)
-        if not focused:
-            raise ValueError("--profile-candidate requires an explicit focused case list")
-        if len(focused) > PROFILE_MAX_CASES:
-            raise ValueError(f"--profile-candidate accepts at most {PROFILE_MAX_CASES} focused cases")
         if device.type != "cuda" and not args.encoder_configs:
             raise ValueError("--profile-candidate requires a GPU device")
         if args.benchmark_on_failure:
@@ -180,6 +196,20 @@ def validate_args(args: argparse.Namespace, device: torch.device, dtype: torch.d
         raise ValueError("cpu_baseline_seconds must be non-negative")
     if device.type == "cpu" and dtype == torch.float16:
         print("[warning] float16 CPU kernels may be unsupported or slow")
+
+
+def validate_profile_focus(args: argparse.Namespace) -> None:
+    """The checks on --profile-candidate / --rocprof that need no device."""
+    if args.rocprof and not args.profile_candidate:
+        raise ValueError("--rocprof requires --profile-candidate")
+    if args.profile_candidate:
+        focused = args.encoder_configs or (args.official_cases if args.official_matrix else None)
+        if not focused:
+            raise ValueError("--profile-candidate requires an explicit focused case list")
+        if len(focused) > PROFILE_MAX_CASES:
+            raise ValueError(f"--profile-candidate accepts at most {PROFILE_MAX_CASES} focused cases")
+    if args.rocprof_timeout <= 0:
+        raise ValueError("rocprof_timeout must be positive")
 
 
 def environment_metadata(device: torch.device, dtype: torch.dtype) -> Dict[str, object]:
@@ -231,6 +261,8 @@ def settings_metadata(args: argparse.Namespace) -> Dict[str, object]:
             "profiled_replays": PROFILE_CANDIDATE_REPLAYS,
             "event_limit": PROFILE_MAX_EVENTS,
         }
+        if args.rocprof:
+            settings["candidate_profile"]["rocprof_passes"] = [name for name, _ in ROCPROF_PASSES]
     return settings
 
 
@@ -315,9 +347,10 @@ def cpu_baseline(baseline_cpu: nn.Module, config: TransformerConfig, dtype: torc
 
 # ------------------------------------------------------------------ cases ----
 
-def _run_benchmark_case_with_profile(
-    config: TransformerConfig, args: argparse.Namespace, device: torch.device, dtype: torch.dtype,
-) -> Tuple[AccuracySummary, Optional[Dict[str, object]], Optional[Dict[str, object]]]:
+def build_models(config: TransformerConfig, args: argparse.Namespace,
+                 device: torch.device) -> Tuple[nn.Module, nn.Module]:
+    """Seed, then the baseline, then the candidate, then the strict weight
+    copy (runner.py:304-326 of the reference); both still on the host."""
     config.validate()
     torch.manual_seed(args.seed)
     if device.type == "cuda":
@@ -325,6 +358,13 @@ def _run_benchmark_case_with_profile(
     baseline = BaselineTransformer(config)
     optimized = UserOptimizedTransformer(config)
     copy_model_weights(baseline, optimized, strict=not args.non_strict_weight_copy)
+    return baseline, optimized
+
+
+def _run_benchmark_case_with_profile(
+    config: TransformerConfig, args: argparse.Namespace, device: torch.device, dtype: torch.dtype,
+) -> Tuple[AccuracySummary, Optional[Dict[str, object]], Optional[Dict[str, object]]]:
+    baseline, optimized = build_models(config, args, device)
     baseline_cpu = None
     if args.cpu_baseline_seconds > 0:
         baseline_cpu = BaselineTransformer(config)
@@ -467,7 +507,8 @@ def is_out_of_memory_error(error: BaseException) -> bool:
 
 
 def _run_matrix(cases: List[Tuple[int, TransformerConfig, argparse.Namespace, torch.device, torch.dtype]],
-                args: argparse.Namespace, device: torch.device, dtype: torch.dtype, case_set: str) -> int:
+                args: argparse.Namespace, device: torch.device, dtype: torch.dtype, case_set: str,
+                rocprof: Optional[Dict[int, Dict[str, object]]] = None) -> int:
     requested = [case_id for case_id, *_ in cases]
     results: List[Dict[str, object]] = []
     for position, (case_id, config, case_args, case_device, case_dtype) in enumerate(cases, start=1):
@@ -475,6 +516,8 @@ def _run_matrix(cases: List[Tuple[int, TransformerConfig, argparse.Namespace, to
         try:
             accuracy, performance, profile = _run_benchmark_case_with_profile(
                 config, case_args, case_device, case_dtype)
+            if profile is not None and rocprof is not None and case_id in rocprof:
+                profile["rocprof"] = rocprof[case_id]
             result = official_case_result(case_id, config, accuracy, performance, profile)
         except UnsupportedShapeError as error:
             print(f"[unsupported shape] case {case_id}: {error}")
@@ -494,10 +537,15 @@ def _run_matrix(cases: List[Tuple[int, TransformerConfig, argparse.Namespace, to
     return 0
 
 
-def run_official_matrix(args: argparse.Namespace, device: torch.device, dtype: torch.dtype) -> int:
+def official_cases(args: argparse.Namespace, device: torch.device, dtype: torch.dtype):
     requested = args.official_cases or list(range(1, len(OFFICIAL_TEST_CASES) + 1))
-    cases = [(cid, OFFICIAL_TEST_CASES[cid - 1], args, device, dtype) for cid in requested]
-    return _run_matrix(cases, args, device, dtype, "competition_appendix_3_7")
+    return [(cid, OFFICIAL_TEST_CASES[cid - 1], args, device, dtype) for cid in requested]
+
+
+def run_official_matrix(args: argparse.Namespace, device: torch.device, dtype: torch.dtype,
+                        rocprof: Optional[Dict[int, Dict[str, object]]] = None) -> int:
+    return _run_matrix(official_cases(args, device, dtype), args, device, dtype, "competition_appendix_3_7",
+                       rocprof)
 
 
 def encoder_config_case(name: str, args: argparse.Namespace) -> Tuple[TransformerConfig, argparse.Namespace,
@@ -511,12 +559,72 @@ def encoder_config_case(name: str, args: argparse.Namespace) -> Tuple[Transforme
     return spec.config, case_args, case_device, spec.dtype
 
 
-def run_encoder_configs(args: argparse.Namespace, device: torch.device, dtype: torch.dtype) -> int:
+def encoder_cases(args: argparse.Namespace):
     cases = []
     for name in args.encoder_configs:
         config, case_args, case_device, case_dtype = encoder_config_case(name, args)
         cases.append((ENCODER_CONFIG_NAMES.index(name) + 1, config, case_args, case_device, case_dtype))
-    return _run_matrix(cases, args, device, dtype, "mi355x_encoder_configs_c1_c5")
+    return cases
+
+
+def run_encoder_configs(args: argparse.Namespace, device: torch.device, dtype: torch.dtype,
+                        rocprof: Optional[Dict[int, Dict[str, object]]] = None) -> int:
+    return _run_matrix(encoder_cases(args), args, device, dtype, "mi355x_encoder_configs_c1_c5", rocprof)
+
+
+def profiled_case_ids(args: argparse.Namespace) -> List[int]:
+    """Case ids of the focused cases that run on the GPU, in run order,
+    decided without touching the GPU."""
+    if args.encoder_configs:
+        return [ENCODER_CONFIG_NAMES.index(n) + 1 for n in args.encoder_configs
+                if ENCODER_CONFIGS[n].device_type != "cpu"]
+    return list(args.official_cases or [])
+
+
+def collect_rocprof(args: argparse.Namespace, argv: Sequence[str]) -> Dict[int, Dict[str, object]]:
+    """Run the rocprofv3 passes over child processes that replay the focused
+    cases (before this process touches the GPU) and summarise them per case."""
+    case_ids = profiled_case_ids(args)
+    if not case_ids:
+        return {}
+    out_dir = str(args.rocprof_dir) if args.rocprof_dir else tempfile.mkdtemp(prefix="rocprof_candidate_")
+    print(f"=== rocprofv3 candidate profile ({len(case_ids)} case(s), output {out_dir}) ===", flush=True)
+    commands = run_rocprof_passes(out_dir, list(argv), args.rocprof_timeout,
+                                  log=lambda line: print(line, flush=True))
+    summaries = summarize_rocprof({name: os.path.join(out_dir, name) for name, _ in ROCPROF_PASSES},
+                                  commands, len(case_ids))
+    for summary in summaries:
+        summary["output_dir"] = out_dir
+    return dict(zip(case_ids, summaries))
+
+
+def run_rocprof_child(args: argparse.Namespace) -> int:
+    """The profiled program of one rocprofv3 pass: for every focused GPU
+    case, two warmup calls, then three candidate calls between two marker
+    dispatches; a calibration copy of known size comes first."""
+    device = resolve_device(args.device)
+    dtype = resolve_dtype(args.dtype)
+    configure_runtime(args, device)
+    cases = encoder_cases(args) if args.encoder_configs else official_cases(args, device, dtype)
+    calibration_copy()
+    for case_id, config, case_args, case_device, case_dtype in cases:
+        if case_device.type != "cuda":
+            continue
+        _, optimized = build_models(config, case_args, case_device)
+        optimized = optimized.to(device=case_device, dtype=case_dtype).eval()
+        x, mask = generate_random_case(config, case_device, case_dtype, case_args.seed + 200000,
+                                       case_args.padding_ratio, case_args.input_scale)
+        warmup_model(optimized, x, mask, PROFILE_WARMUP_REPLAYS, case_device)
+        region_marker()
+        with torch.inference_mode():
+            for _ in range(PROFILE_CANDIDATE_REPLAYS):
+                optimized(x, mask)
+        region_marker()
+        torch.cuda.synchronize(case_device)
+        print(f"profiled case {case_id}", flush=True)
+        del optimized, x, mask
+        release_case_memory(case_device)
+    return 0
 
 
 def run_single_case(args: argparse.Namespace, device: torch.device, dtype: torch.dtype) -> int:
@@ -527,13 +635,25 @@ def run_single_case(args: argparse.Namespace, device: torch.device, dtype: torch
 
 
 def main(argv: Optional[Sequence[str]] = None) -> int:
+    argv = list(sys.argv[1:] if argv is None else argv)
     args = parse_args(argv)
+    if args.rocprof_child:
+        return run_rocprof_child(args)
+    rocprof = None
+    if args.rocprof:
+        # before anything below touches the GPU
+        validate_profile_focus(args)
+        rocprof = collect_rocprof(args, argv)
     device = resolve_device(args.device)
     dtype = resolve_dtype(args.dtype)
     validate_args(args, device, dtype)
     configure_runtime(args, device)
     if args.encoder_configs:
-        return run_encoder_configs(args, device, dtype)
+        return run_encoder_configs(args, device, dtype, rocprof)
     if args.official_matrix:
-        return run_official_matrix(args, device, dtype)
+        return run_official_matrix(args, device, dtype, rocprof)
     return run_single_case(args, device, dtype)
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())
