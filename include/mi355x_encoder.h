@@ -77,6 +77,34 @@ int enc_linear_bf16(const void* a, const void* weight, const void* bias,
                     int64_t out_features, int64_t in_features, int32_t epilogue,
                     const uint8_t* row_mask, void* stream);
 
+/* Tile-packed copy of an nn.Linear weight W[out_features, in_features] for
+ * the wide GEMM kernel: element (n, k) moves to
+ *   ((n / P * (in_features / 32) + k / 32) * P + n % P) * 32 + k % 32,
+ * P = 256 when out_features % 256 == 0, else 128, so each 32-deep K slice of a
+ * P-row group of W is one contiguous block (one 1 KiB run per load
+ * instruction instead of 64-byte pieces of rows in_features apart).  packed
+ * holds out_features * in_features bf16 elements and must not alias weight;
+ * out_features % 128 == 0, in_features % 32 == 0, both pointers 16-byte
+ * aligned.  The copy is a pure permutation: every product computed from it is
+ * bitwise the product computed from weight.  Replaces the load-time weight
+ * packing of transformer_benchmark/models.py:105-158 and copy_model_weights
+ * (:1242-1255) on the candidate side, whose packed [3D, D] QKV weight this
+ * library takes as the plain weight; the tile layout is this library's. */
+int enc_prepack_weight_bf16(const void* weight, void* packed,
+                            int64_t out_features, int64_t in_features,
+                            void* stream);
+
+/* enc_linear_bf16 with the weight's tile-packed copy (enc_prepack_weight_bf16
+ * of weight) beside it: the wide kernel reads packed_weight, the kernels for
+ * few rows read weight; the result is bitwise that of enc_linear_bf16.
+ * out_features % 128 == 0.  Same reference code as enc_linear_bf16. */
+int enc_linear_prepacked_bf16(const void* a, const void* weight,
+                              const void* packed_weight, const void* bias,
+                              const void* residual, void* out, int64_t rows,
+                              int64_t out_features, int64_t in_features,
+                              int32_t epilogue, const uint8_t* row_mask,
+                              void* stream);
+
 /* Packed QKV projection x[batch*seq_len, d_model] . qkv_weight[3*d_model,
  * d_model]^T + qkv_bias, rounded to bf16 and written head-major:
  *   q, k : [batch, num_heads, seq_len, head_dim]
@@ -151,6 +179,10 @@ int enc_mask_lengths(const uint8_t* mask, int64_t batch, int64_t seq_len,
                                       runs final_norm (enc_layernorm_bf16,
                                       with row_mask), e.g. into a fresh
                                       tensor after a graph replay           */
+#define ENC_FWD_PACKED_WEIGHTS 4   /* weights carries 4 * num_layers more
+                                      pointers: the enc_prepack_weight_bf16
+                                      copies of each layer's qkv_proj,
+                                      out_proj, ffn_in and ffn_out weights  */
 
 /* Bytes of device workspace enc_encoder_forward_bf16 needs for this shape. */
 int64_t enc_encoder_workspace_bytes(int64_t batch, int64_t seq_len,
@@ -163,7 +195,9 @@ int64_t enc_encoder_workspace_bytes(int64_t batch, int64_t seq_len,
  *   norm1.weight, norm1.bias, qkv_proj.weight [3D,D], qkv_proj.bias [3D],
  *   out_proj.weight, out_proj.bias, norm2.weight, norm2.bias,
  *   ffn_in.weight [F,D], ffn_in.bias, ffn_out.weight [D,F], ffn_out.bias,
- * followed by final_norm.weight, final_norm.bias.
+ * followed by final_norm.weight, final_norm.bias; with ENC_FWD_PACKED_WEIGHTS,
+ * then per layer the packed qkv_proj, out_proj, ffn_in and ffn_out weights
+ * (3*d_model, d_model and ffn_dim must then be multiples of 128).
  * Masking follows the reference: with row_mask non-null, padded rows of the
  * attention output are zero (models.py:78-79), block outputs are zeroed on
  * padded rows (models.py:736-737) and so is the final output

@@ -222,6 +222,68 @@ def test_graph_survives_eager_call_at_another_shape(device):
         del filler
 
 
+def _unpacked_forward(candidate, x, mask=None):
+    """The native forward from the plain weights only (no packed copies)."""
+    cfg = candidate.config
+    table, eps, packed = candidate._native_weights(x.device, 0)
+    assert not packed
+    b, s, d = x.shape
+    workspace = torch.empty(native.encoder_workspace_bytes(b, s, d, cfg.num_heads, cfg.ffn_dim),
+                            device=x.device, dtype=torch.uint8)
+    out = torch.empty_like(x)
+    kv_len = row_mask = None
+    if mask is not None and not bool(mask.all()):
+        kv_len = native.mask_lengths(mask)
+        row_mask = mask.contiguous().view(torch.uint8)
+    native.encoder_forward(x, out, workspace, table, cfg.num_heads, cfg.ffn_dim, cfg.num_layers, eps,
+                           cfg.causal, kv_len, None, row_mask)
+    return out
+
+
+def test_encoder_packed_weights_bitwise_unpacked(device):
+    """c4 (prefix padding, causal): the forward over the tile-packed weight
+    copies equals the forward over the plain weights bit for bit."""
+    spec = ENCODER_CONFIGS["c4"]
+    cfg = spec.config
+    _, candidate = build_models(cfg, spec.seed, device)
+    with torch.inference_mode():
+        x, mask = generate_random_case(cfg, device, torch.bfloat16, spec.seed + 5, spec.padding_ratio, 1.0)
+        packed = candidate(x, mask)
+        assert candidate._hip.packed is not None and len(candidate._hip.packed_views) == 4 * cfg.num_layers
+        plain = _unpacked_forward(candidate, x, mask)
+        torch.cuda.synchronize()
+    mismatches = int((packed.view(torch.int16) != plain.view(torch.int16)).sum())
+    print(f"[packed] c4: {mismatches} mismatches against the plain-weight forward", flush=True)
+    assert mismatches == 0
+
+
+@pytest.mark.parametrize("graph", [False, True], ids=["eager", "graph"])
+def test_packed_copies_follow_in_place_weight_updates(device, graph):
+    """An in-place weight update after a forward is seen by the next forward:
+    the packed copies are remade (eager), and the graph, whose kernels read
+    them, is captured again."""
+    cfg = TransformerConfig(1, 2048, 256, 4, 1024, 2, True)  # 2048 rows: packed, graph-eligible
+    _, candidate = build_models(cfg, 13, device)
+    seq = cfg.seq_len if graph else 1536  # another length runs eagerly
+    g = torch.Generator(device=device).manual_seed(3)
+    with torch.inference_mode():
+        x = torch.randn(1, seq, cfg.d_model, generator=g, device=device).bfloat16()
+        before = candidate(x)
+        assert (candidate._cuda_graph is not None) == graph
+        captures = candidate._cuda_graph_capture_count
+        candidate.layers[1].ffn_in.weight.mul_(0.5)
+        candidate.layers[0].attention.qkv_proj.weight.add_(0.01)
+        after = candidate(x)
+        torch.cuda.synchronize()
+        plain = _unpacked_forward(candidate, x)
+        torch.cuda.synchronize()
+        if graph:
+            assert candidate._cuda_graph_capture_count == captures + 1
+            assert torch.equal(candidate(x), plain)  # replay of the new capture
+    assert not torch.equal(before, after)
+    assert torch.equal(after, plain)
+
+
 def test_online_attention_encoder_stays_close(device):
     """The opt-in one-pass attention: its bf16 weight-rounding noise compounds
     over the layers, so it is held to a looser bound than the reference's gate

@@ -242,6 +242,63 @@ def test_linear_streamk_tail_bitwise(device, m):
         assert torch.equal(part.view(32, 100000, 16, 64).permute(0, 2, 3, 1), v_t[..., :100000])
 
 
+@pytest.mark.parametrize("n,k", [(3072, 1024), (1024, 1024), (4096, 1024), (1024, 4096), (1536, 512), (384, 256),
+                                 (128, 32)])
+def test_prepack_weight_layout(device, n, k):
+    """The packed copy is W[N, K] regrouped as [N / P][K / 32][P][32] (P = 256
+    when N % 256 == 0, else 128): a pure permutation, checked against the same
+    regrouping done with torch views."""
+    g = torch.Generator(device=device).manual_seed(n + k)
+    w = torch.randn(n, k, generator=g, device=device).bfloat16()
+    p = native.prepack_rows(n, k)
+    assert p == (256 if n % 256 == 0 else 128)
+    ref = w.view(n // p, p, k // 32, 32).permute(0, 2, 1, 3).reshape(-1)
+    assert torch.equal(native.prepack_weight(w), ref)
+
+
+@pytest.mark.parametrize(
+    "m,n,k,epi",
+    [
+        (8192, 3072, 1024, native.ENC_EPI_BIAS),               # 256x128x64 tiles (c3 qkv rows)
+        (32768, 3072, 1024, native.ENC_EPI_BIAS),              # 256x256x32 (c4 qkv)
+        (32768, 4096, 1024, native.ENC_EPI_BIAS_GELU),         # 256x128x32, two per CU (ffn_in)
+        (32768, 1024, 4096, native.ENC_EPI_BIAS_RESIDUAL_ZERO),
+        (32768, 1024, 1024, native.ENC_EPI_BIAS_RESIDUAL_KEEP),
+        (5000, 384, 256, native.ENC_EPI_BIAS),                 # P = 128, ragged last tile row
+        (1100, 128, 1024, native.ENC_EPI_BIAS),                # 128x128x64 tiles
+        (100000, 1024, 1024, native.ENC_EPI_BIAS),             # stream-K tail rows read the plain weight
+        (200, 1024, 1024, native.ENC_EPI_BIAS),                # few rows: the packed copy goes unread
+    ],
+)
+def test_linear_prepacked_is_bitwise_the_plain_product(device, m, n, k, epi):
+    g = torch.Generator(device=device).manual_seed(m + n + k)
+    a = torch.randn(m, k, generator=g, device=device).bfloat16()
+    w = ((torch.rand(n, k, generator=g, device=device) * 2 - 1) / math.sqrt(k)).bfloat16()
+    bias = ((torch.rand(n, generator=g, device=device) * 2 - 1) / 32).bfloat16()
+    residual = mask = None
+    if epi in (native.ENC_EPI_BIAS_RESIDUAL_KEEP, native.ENC_EPI_BIAS_RESIDUAL_ZERO):
+        residual = torch.randn(m, n, generator=g, device=device).bfloat16()
+        mask = torch.rand(m, generator=g, device=device) > 0.3
+    plain = native.linear(a, w, bias, epi, residual=residual, row_mask=mask)
+    packed = native.linear(a, w, bias, epi, residual=residual, row_mask=mask, packed_weight=native.prepack_weight(w))
+    mismatches = int((plain.view(torch.int16) != packed.view(torch.int16)).sum())
+    print(f"[prepack] {m}x{n}x{k} epi {epi}: {mismatches} mismatches", flush=True)
+    assert mismatches == 0
+    if epi == native.ENC_EPI_BIAS:
+        assert torch.equal(packed, F.linear(a, w, bias))
+
+
+def test_linear_prepacked_rejects_unpackable_shapes(device):
+    a = torch.zeros(2048, 1024, device=device, dtype=torch.bfloat16)
+    w = torch.zeros(96, 1024, device=device, dtype=torch.bfloat16)
+    bias = torch.zeros(96, device=device, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="no packed form"):
+        native.prepack_weight(w)
+    with pytest.raises(native.EncoderKernelError, match="out_features % 128") as info:
+        native.linear(a, w, bias, packed_weight=torch.zeros(96 * 1024, device=device, dtype=torch.bfloat16))
+    assert info.value.code == native.ENC_ERR_UNSUPPORTED
+
+
 @pytest.mark.parametrize(
     "b,s,d,h",
     [(1, 128, 512, 8), (2, 100, 512, 8), (8, 1024, 1024, 16), (3, 37, 1024, 16), (64, 128, 32, 4), (3, 37, 128, 16),

@@ -278,3 +278,43 @@ def test_noalloc_entry_point_rejects_large_shapes_before_any_device_call():
     assert rc == native.ENC_ERR_UNSUPPORTED
     assert b"scratch array" in lib.enc_last_error()
     assert lib.enc_encoder_workspace_bytes(8, 1024, 1024, 16, 4096) > native.NOALLOC_SCRATCH_BYTES
+
+
+def test_prepack_argument_checks_match_the_python_rule():
+    """enc_prepack_weight_bf16 rejects every shape without a packed form before
+    any device call, exactly where native.prepack_rows says there is none."""
+    lib = native.load_library()
+    fake_w, fake_p = ctypes.c_void_p(4096), ctypes.c_void_p(8192)
+    for n in (32, 96, 128, 200, 256, 384, 1000, 1024, 1536, 3072):
+        for k in (16, 32, 48, 1024):
+            if native.prepack_rows(n, k):
+                assert native.prepack_rows(n, k) == (256 if n % 256 == 0 else 128)
+                continue
+            rc = lib.enc_prepack_weight_bf16(fake_w, fake_p, n, k, None)
+            assert rc == native.ENC_ERR_UNSUPPORTED, (n, k)
+    assert lib.enc_prepack_weight_bf16(fake_w, fake_w, 256, 32, None) == native.ENC_ERR_INVALID  # aliasing
+    assert lib.enc_prepack_weight_bf16(None, fake_p, 256, 32, None) == native.ENC_ERR_INVALID
+
+
+def test_encoder_packed_flag_needs_the_packed_pointers():
+    """With ENC_FWD_PACKED_WEIGHTS the table holds 4 more pointers per layer;
+    a null one among them, or a shape without a packed form, is rejected
+    before any device call."""
+    lib = native.load_library()
+    layers = 2
+    n_ptrs = 16 * layers + 2
+    ptrs = [64 * (i + 1) for i in range(n_ptrs)]
+    ptrs[12 * layers + 2 + 5] = 0  # layer 1's packed out_proj weight
+    table = (ctypes.c_void_p * n_ptrs)(*ptrs)
+    fake = ctypes.c_void_p(16)
+    ws = ctypes.c_void_p(1 << 20)
+    rc = lib.enc_encoder_forward_bf16(fake, fake, ws, 1 << 40, ctypes.cast(table, ctypes.c_void_p), 1, 2048, 1024,
+                                      16, 4096, layers, 1e-5, 1, None, None, None, native.ENC_FWD_PACKED_WEIGHTS,
+                                      None)
+    assert rc == native.ENC_ERR_INVALID and b"index 31" in lib.enc_last_error()
+    table = (ctypes.c_void_p * (16 + 2))(*([64] * 18))
+    rc = lib.enc_encoder_forward_bf16(fake, fake, ws, 1 << 40, ctypes.cast(table, ctypes.c_void_p), 1, 2048, 1024,
+                                      16, 4000, 1, 1e-5, 1, None, None, None, native.ENC_FWD_PACKED_WEIGHTS, None)
+    assert rc == native.ENC_ERR_UNSUPPORTED and b"packed weights" in lib.enc_last_error()
+    with pytest.raises(ValueError, match="18 device pointers"):
+        native._forward_flags(False, True, True, torch.zeros(14, dtype=torch.int64), 1)

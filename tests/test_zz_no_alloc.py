@@ -27,7 +27,7 @@ def _model(cfg, seed, device):
 
 def _both(model, x, mask):
     cfg = model.config
-    table, eps = model._native_weights(x.device)
+    table, eps, packed = model._native_weights(x.device, x.shape[0] * x.shape[1])
     kv_len = row_mask = None
     if mask is not None and not bool(mask.all()):
         kv_len = native.mask_lengths(mask)
@@ -37,10 +37,10 @@ def _both(model, x, mask):
                             device=x.device, dtype=torch.uint8)
     ref = torch.empty_like(x)
     native.encoder_forward(x, ref, workspace, table, cfg.num_heads, cfg.ffn_dim, cfg.num_layers, eps,
-                           cfg.causal, kv_len, None, row_mask)
+                           cfg.causal, kv_len, None, row_mask, packed_weights=packed)
     out = torch.full_like(x, float("nan"))
     native.encoder_forward_noalloc(x, out, table, cfg.num_heads, cfg.ffn_dim, cfg.num_layers, eps,
-                                   cfg.causal, kv_len, None, row_mask)
+                                   cfg.causal, kv_len, None, row_mask, packed_weights=packed)
     torch.cuda.synchronize()
     return ref, out
 
@@ -71,7 +71,7 @@ def test_noalloc_rejects_shapes_above_the_scratch_array(device):
     assert need > native.NOALLOC_SCRATCH_BYTES
     model = _model(TransformerConfig(cfg.batch_size, cfg.seq_len, cfg.d_model, cfg.num_heads, cfg.ffn_dim, 1,
                                      cfg.causal), spec.seed, device)
-    table, eps = model._native_weights(device)
+    table, eps, _ = model._native_weights(device)
     x = torch.zeros(cfg.batch_size, cfg.seq_len, cfg.d_model, device=device, dtype=torch.bfloat16)
     out = torch.empty_like(x)
     with pytest.raises(native.EncoderKernelError, match="scratch array") as info:

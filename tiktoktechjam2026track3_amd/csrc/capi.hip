@@ -143,7 +143,7 @@ namespace {
 int check_encoder_call(const void* x, void* out, const void* const* weights, int64_t batch, int64_t seq_len,
                        int64_t d_model, int64_t num_heads, int64_t ffn_dim, int64_t num_layers, float eps,
                        const int32_t* kv_len, const uint8_t* key_mask, int32_t flags, EncoderWorkspace* plan) {
-  if (flags & ~(ENC_FWD_ONLINE_ATTENTION | ENC_FWD_SKIP_FINAL_NORM))
+  if (flags & ~(ENC_FWD_ONLINE_ATTENTION | ENC_FWD_SKIP_FINAL_NORM | ENC_FWD_PACKED_WEIGHTS))
     return fail(ENC_ERR_INVALID, "encoder: unknown flags");
   const bool final_norm = (flags & ENC_FWD_SKIP_FINAL_NORM) == 0;
   if (!final_norm && num_layers < 1) return fail(ENC_ERR_INVALID, "encoder: skipping final_norm needs a layer");
@@ -154,8 +154,17 @@ int check_encoder_call(const void* x, void* out, const void* const* weights, int
   if (!x || !out || !weights) return fail(ENC_ERR_INVALID, "encoder: null pointer");
   if (kv_len && key_mask) return fail(ENC_ERR_INVALID, "encoder: pass kv_len or key_mask, not both");
   if (!(eps > 0.f)) return fail(ENC_ERR_INVALID, "encoder: eps must be positive");
-  for (int64_t i = 0; i < 12 * num_layers + 2; ++i)
+  const int64_t num_ptrs = 12 * num_layers + 2 + ((flags & ENC_FWD_PACKED_WEIGHTS) ? 4 * num_layers : 0);
+  for (int64_t i = 0; i < num_ptrs; ++i)
     if (!weights[i]) return fail(ENC_ERR_INVALID, "encoder: null weight pointer at index " + std::to_string(i));
+  if (flags & ENC_FWD_PACKED_WEIGHTS) {
+    // every packed matrix must have the shape's packed form
+    const int64_t shapes[4][2] = {{3 * d_model, d_model}, {d_model, d_model}, {ffn_dim, d_model}, {d_model, ffn_dim}};
+    for (const auto& nk : shapes)
+      if (enc::gemm_prepack_rows(nk[0], nk[1]) == 0)
+        return fail(ENC_ERR_UNSUPPORTED, "encoder: packed weights need out_features % 128 == 0 (got " +
+                                             std::to_string(nk[0]) + " x " + std::to_string(nk[1]) + ")");
+  }
   *plan = plan_workspace(batch, seq_len, d_model, num_heads, ffn_dim);
   return ENC_OK;
 }
@@ -185,6 +194,14 @@ int run_encoder_forward(const void* x, void* out, void* workspace, const Encoder
   const int cus = device_cus();
   const float scale = 1.0f / sqrtf(static_cast<float>(D / H));
   auto W = [&](int64_t layer, int idx) { return static_cast<const bf16_t*>(weights[layer * 12 + idx]); };
+  // Tile-packed copies of the four projection weights (qkv, out, ffn_in,
+  // ffn_out) follow the 12 * num_layers + 2 pointers when asked for.
+  const bool packed = (flags & ENC_FWD_PACKED_WEIGHTS) != 0;
+  auto use_packed = [&](enc::GemmEpilogueArgs& a, int64_t layer, int which, int64_t n, int64_t k) {
+    if (!packed) return;
+    a.w_packed = static_cast<const bf16_t*>(weights[12 * num_layers + 2 + 4 * layer + which]);
+    a.w_packed_rows = enc::gemm_prepack_rows(n, k);
+  };
 
   // Narrow models with up to 8192 tokens run the block tail (out_proj ..
   // ffn_out, and the next layer's norm1) as one kernel, whose 16-byte loads
@@ -218,6 +235,7 @@ int run_encoder_forward(const void* x, void* out, void* workspace, const Encoder
     qa.head_dim = static_cast<int>(D / H);
     qa.d_model = static_cast<int>(D);
     qa.ld_vt = static_cast<int>(enc::vt_stride(seq_len));
+    use_packed(qa, layer, 0, 3 * D, D);
     e = enc::gemm_bf16(ln, W(layer, 2), T, 3 * D, D, enc::kEpiQkvHeadMajor, qa, cus, st);
     if (e != hipSuccess) return fail_hip(e, "encoder qkv");
     // attention -> context [T, D]
@@ -257,6 +275,7 @@ int run_encoder_forward(const void* x, void* out, void* workspace, const Encoder
     oa.residual = cur;
     oa.row_mask = row_mask;
     oa.out = x_attn;
+    use_packed(oa, layer, 1, D, D);
     e = enc::gemm_bf16(ctx, W(layer, 4), T, D, D, enc::kEpiResidualKeep, oa, cus, st);
     if (e != hipSuccess) return fail_hip(e, "encoder out_proj");
     // norm2
@@ -266,6 +285,7 @@ int run_encoder_forward(const void* x, void* out, void* workspace, const Encoder
     enc::GemmEpilogueArgs fa;
     fa.bias = W(layer, 9);
     fa.out = hidden;
+    use_packed(fa, layer, 2, F, D);
     e = enc::gemm_bf16(ln, W(layer, 8), T, F, D, enc::kEpiBiasGelu, fa, cus, st);
     if (e != hipSuccess) return fail_hip(e, "encoder ffn_in");
     // ffn_out + residual; padded rows are zeroed (block output masked_fill)
@@ -275,6 +295,7 @@ int run_encoder_forward(const void* x, void* out, void* workspace, const Encoder
     fo.residual = x_attn;
     fo.row_mask = row_mask;
     fo.out = x_next;
+    use_packed(fo, layer, 3, D, F);
     e = enc::gemm_bf16(hidden, W(layer, 10), T, D, F, enc::kEpiResidualZero, fo, cus, st);
     if (e != hipSuccess) return fail_hip(e, "encoder ffn_out");
     cur = x_next;
@@ -311,9 +332,13 @@ int enc_layernorm_bf16(const void* x, const void* gamma, const void* beta, void*
   return ok();
 }
 
-int enc_linear_bf16(const void* a, const void* weight, const void* bias, const void* residual,
-                    void* out, int64_t rows, int64_t out_features, int64_t in_features,
-                    int32_t epilogue, const uint8_t* row_mask, void* stream) {
+}  // extern "C"
+
+namespace {
+
+int linear_entry(const void* a, const void* weight, const void* packed_weight, const void* bias,
+                 const void* residual, void* out, int64_t rows, int64_t out_features, int64_t in_features,
+                 int32_t epilogue, const uint8_t* row_mask, void* stream) {
   if (epilogue < ENC_EPI_BIAS || epilogue > ENC_EPI_BIAS_RESIDUAL_ZERO)
     return fail(ENC_ERR_INVALID, "linear: unknown epilogue " + std::to_string(epilogue));
   if (rows < 0 || out_features <= 0 || in_features <= 0)
@@ -330,11 +355,55 @@ int enc_linear_bf16(const void* a, const void* weight, const void* bias, const v
   ep.residual = static_cast<const enc::bf16_t*>(residual);
   ep.row_mask = row_mask;
   ep.out = static_cast<enc::bf16_t*>(out);
+  if (packed_weight != nullptr) {
+    ep.w_packed = static_cast<const enc::bf16_t*>(packed_weight);
+    ep.w_packed_rows = enc::gemm_prepack_rows(out_features, in_features);
+    if (ep.w_packed_rows == 0)
+      return fail(ENC_ERR_UNSUPPORTED, "linear: a packed weight needs out_features % 128 == 0 (got " +
+                                           std::to_string(out_features) + ")");
+  }
   hipError_t e = enc::gemm_bf16(static_cast<const enc::bf16_t*>(a), static_cast<const enc::bf16_t*>(weight), rows,
                                 out_features, in_features, epilogue, ep, device_cus(),
                                 static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail_hip(e, "linear launch");
   return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+int enc_linear_bf16(const void* a, const void* weight, const void* bias, const void* residual,
+                    void* out, int64_t rows, int64_t out_features, int64_t in_features,
+                    int32_t epilogue, const uint8_t* row_mask, void* stream) {
+  return linear_entry(a, weight, nullptr, bias, residual, out, rows, out_features, in_features, epilogue, row_mask,
+                      stream);
+}
+
+int enc_prepack_weight_bf16(const void* weight, void* packed, int64_t out_features, int64_t in_features,
+                            void* stream) {
+  if (out_features <= 0 || in_features <= 0) return fail(ENC_ERR_INVALID, "prepack: features must be > 0");
+  if (!weight || !packed) return fail(ENC_ERR_INVALID, "prepack: null tensor pointer");
+  if (weight == packed) return fail(ENC_ERR_INVALID, "prepack: packed must not alias weight");
+  if (enc::gemm_prepack_rows(out_features, in_features) == 0)
+    return fail(ENC_ERR_UNSUPPORTED, "prepack: out_features must be a multiple of 128 and in_features of 32 (got " +
+                                         std::to_string(out_features) + " x " + std::to_string(in_features) + ")");
+  if (out_features * in_features > (int64_t(1) << 31))
+    return fail(ENC_ERR_UNSUPPORTED, "prepack: at most 2^31 elements");
+  if (reinterpret_cast<uintptr_t>(weight) % 16 != 0 || reinterpret_cast<uintptr_t>(packed) % 16 != 0)
+    return fail(ENC_ERR_INVALID, "prepack: weight and packed must be 16-byte aligned");
+  hipError_t e = enc::gemm_prepack_weight(static_cast<const enc::bf16_t*>(weight), static_cast<enc::bf16_t*>(packed),
+                                          out_features, in_features, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail_hip(e, "prepack launch");
+  return ok();
+}
+
+int enc_linear_prepacked_bf16(const void* a, const void* weight, const void* packed_weight, const void* bias,
+                              const void* residual, void* out, int64_t rows, int64_t out_features,
+                              int64_t in_features, int32_t epilogue, const uint8_t* row_mask, void* stream) {
+  if (!packed_weight) return fail(ENC_ERR_INVALID, "linear: null packed weight");
+  return linear_entry(a, weight, packed_weight, bias, residual, out, rows, out_features, in_features, epilogue,
+                      row_mask, stream);
 }
 
 int enc_qkv_proj_bf16(const void* x, const void* weight, const void* bias, void* q, void* k, void* v_t,

@@ -446,8 +446,18 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
   // captured by the loading lambda makes clang's host pass drop the kernel's
   // launch stub.)
   const char* a_tile = reinterpret_cast<const char*>(A + static_cast<int64_t>(m0) * K);
-  const char* w_tile = reinterpret_cast<const char*>(W + static_cast<int64_t>(n0) * K);
   const int a_rows_left = M - 1 - m0;  // rows past M re-load the last row, never stored
+  // W comes from nn.Linear's [N, K] layout (row stride K) or from the
+  // tile-packed copy [N / PN][K / 32][PN][32] (gemm_prepack_weight), where the
+  // tile's rows of one 32-deep K slice are contiguous: row r, column c of
+  // stage k0 sits at group base + k0 * PN + (c / 32) * PN * 32 + (n0 % PN + r)
+  // * 32 + c % 32 elements.  Same values in the same LDS slots either way.
+  const bool w_packed = ep.w_packed != nullptr;
+  const int pn = ep.w_packed_rows;
+  const char* w_tile = w_packed ? reinterpret_cast<const char*>(ep.w_packed + static_cast<int64_t>(n0 - n0 % pn) * K)
+                                : reinterpret_cast<const char*>(W + static_cast<int64_t>(n0) * K);
+  const int w_k_mul = w_packed ? pn : 1;  // element step of W per unit of k0
+  const int w_row0 = w_packed ? n0 % pn : 0;
 
   f32x16 acc[RM][RN];
 #pragma unroll
@@ -485,9 +495,11 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
       if (q < part * kPer || q >= (part + 1) * kPer) continue;
       const bool is_a = q < T::kLoadsA;
       const int row = T::kRowsPerLoad * (4 * (is_a ? q : q - T::kLoadsA) + wave);
-      const uint32_t off = is_a ? static_cast<uint32_t>(min(row + lrow, a_rows_left) * K + gcol) * 2u
-                                : static_cast<uint32_t>((row + lrow) * K + gcol) * 2u;
-      __builtin_amdgcn_global_load_lds((is_a ? a_tile : w_tile) + 2 * k0 + off,
+      const uint32_t off =
+          is_a ? static_cast<uint32_t>(min(row + lrow, a_rows_left) * K + gcol) * 2u
+          : w_packed ? static_cast<uint32_t>((gcol >> 5) * pn * 32 + (w_row0 + row + lrow) * 32 + (gcol & 31)) * 2u
+                     : static_cast<uint32_t>((row + lrow) * K + gcol) * 2u;
+      __builtin_amdgcn_global_load_lds((is_a ? a_tile + 2 * k0 : w_tile + 2 * k0 * w_k_mul) + off,
                                        sa + (is_a ? 0 : BM * BK) + row * BK, 16, 0, 0);
     }
   };
@@ -1190,7 +1202,9 @@ hipError_t launch_tail_split(const bf16_t* A, const bf16_t* W, int M, int N, int
 int pick_big_tile(int64_t M, int64_t N, const bf16_t* A, const bf16_t* W, const GemmEpilogueArgs& ep,
                   bool ep_overlaps, int num_cus) {
   auto al = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
-  if (!al(A) || !al(W) || !al(ep.out) || !al(ep.residual) || !al(ep.q) || !al(ep.k) || !al(ep.v_t)) return 0;
+  if (!al(A) || !al(W) || !al(ep.out) || !al(ep.residual) || !al(ep.q) || !al(ep.k) || !al(ep.v_t) ||
+      !al(ep.w_packed))
+    return 0;
   if (M < 1024) return 0;
   const int64_t t256x128 = ((M + 255) / 256) * (N / 128);
   // With two resident 256x128 tiles per CU one tile's epilogue overlaps the
@@ -1213,6 +1227,39 @@ int pick_big_tile(int64_t M, int64_t N, const bf16_t* A, const bf16_t* W, const 
 }
 
 }  // namespace
+
+namespace {
+
+// One 16-byte chunk (8 elements of one row) per thread: reads are row-major
+// W, writes land in the packed order.
+__global__ void __launch_bounds__(256)
+gemm_prepack_kernel(const bf16_t* __restrict__ W, bf16_t* __restrict__ P, int N, int K, int pn) {
+  const int64_t chunk = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int chunks_per_row = K / 8;
+  if (chunk >= static_cast<int64_t>(N) * chunks_per_row) return;
+  const int n = static_cast<int>(chunk / chunks_per_row);
+  const int k = static_cast<int>(chunk - static_cast<int64_t>(n) * chunks_per_row) * 8;
+  const int64_t dst = ((static_cast<int64_t>(n / pn) * (K / 32) + k / 32) * pn + n % pn) * 32 + k % 32;
+  *reinterpret_cast<u32x4*>(P + dst) = *reinterpret_cast<const u32x4*>(W + static_cast<int64_t>(n) * K + k);
+}
+
+}  // namespace
+
+int gemm_prepack_rows(int64_t N, int64_t K) {
+  if (N <= 0 || K <= 0 || K % 32 != 0) return 0;
+  if (N % 256 == 0) return 256;
+  if (N % 128 == 0) return 128;
+  return 0;
+}
+
+hipError_t gemm_prepack_weight(const bf16_t* W, bf16_t* packed, int64_t N, int64_t K, hipStream_t stream) {
+  const int pn = gemm_prepack_rows(N, K);
+  if (pn == 0 || N * K > (int64_t(1) << 31)) return hipErrorInvalidValue;
+  const int64_t chunks = N * (K / 8);
+  hipLaunchKernelGGL(gemm_prepack_kernel, dim3(static_cast<uint32_t>((chunks + 255) / 256)), dim3(256), 0, stream, W,
+                     packed, static_cast<int>(N), static_cast<int>(K), pn);
+  return hipGetLastError();
+}
 
 void gemm_split_plan(int64_t M, int64_t N, int64_t K, int* split, int* chunk) {
   // The reduction order torch.nn.functional.linear (hipBLASLt on ROCm 7) uses
@@ -1321,6 +1368,8 @@ hipError_t gemm_bf16_plain(const bf16_t* A, const bf16_t* W, int64_t M, int64_t 
 
 hipError_t gemm_bf16(const bf16_t* A, const bf16_t* W, int64_t M, int64_t N, int64_t K, int epi,
                      const GemmEpilogueArgs& ep, int num_cus, hipStream_t stream) {
+  // a packed copy must be the one gemm_prepack_weight writes for this shape
+  if (ep.w_packed != nullptr && ep.w_packed_rows != gemm_prepack_rows(N, K)) return hipErrorInvalidValue;
   const StreamKTail* tail = find_streamk_tail(M, N, K, epi);
   if (tail == nullptr) return gemm_bf16_plain(A, W, M, N, K, epi, ep, num_cus, stream);
   // rows before the library's stream-K tail as usual, the tail's rows split

@@ -31,6 +31,10 @@ struct GemmEpilogueArgs {
   int head_dim = 0;
   int d_model = 0;
   int ld_vt = 0;
+  // Optional tile-packed copy of W (gemm_prepack_weight), read by the wide
+  // kernel in place of W; the other kernels read W.
+  const bf16_t* w_packed = nullptr;
+  int w_packed_rows = 0;  // its row-group height PN (gemm_prepack_rows)
 };
 
 // LayerNorm
@@ -44,6 +48,15 @@ hipError_t layernorm_bf16(const bf16_t* x, const bf16_t* gamma, const bf16_t* be
 bool gemm_supported(int64_t M, int64_t N, int64_t K);
 hipError_t gemm_bf16(const bf16_t* A, const bf16_t* W, int64_t M, int64_t N, int64_t K,
                      int epilogue, const GemmEpilogueArgs& ep, int num_cus, hipStream_t stream);
+
+// Tile-packed weight layout for the wide kernel: W[N, K] (nn.Linear layout)
+// as [N / PN][K / 32][PN][32], i.e. element (n, k) at
+//   ((n / PN * (K / 32) + k / 32) * PN + n % PN) * 32 + k % 32,
+// so every 32-deep K stage of a PN-row group (and of any 128-row half of it)
+// is one contiguous block.  gemm_prepack_rows returns PN (256 when N % 256 ==
+// 0, else 128 when N % 128 == 0) or 0 when the shape has no packed form.
+int gemm_prepack_rows(int64_t N, int64_t K);
+hipError_t gemm_prepack_weight(const bf16_t* W, bf16_t* packed, int64_t N, int64_t K, hipStream_t stream);
 
 // Tile shape the dispatcher picks for (M, N) on a device with num_cus CUs.
 void gemm_pick_tile(int64_t M, int64_t N, int epilogue, int num_cus, int* bm, int* bn);

@@ -57,6 +57,9 @@ def even_row_block(seq_len: int, limit: int) -> int:
 
 # Token count up to which the candidate captures a HIP graph (launch-bound shapes).
 GRAPH_MAX_TOKENS = 4096
+# The tile-packed weight copies are read only by the wide GEMM kernel, which
+# runs products of at least this many rows; smaller inputs leave them unmade.
+PACK_MIN_ROWS = 1024
 
 
 class UnsupportedShapeError(NotImplementedError):
@@ -372,6 +375,11 @@ class _HipState:
         self.eps: float = 1e-5
         self.workspace: Optional[torch.Tensor] = None
         self.workspace_key: Optional[Tuple[object, ...]] = None
+        # tile-packed copies of every layer's four projection weights, one flat
+        # buffer, and the (address, version) of each source they were made from
+        self.packed: Optional[torch.Tensor] = None
+        self.packed_views: List[torch.Tensor] = []
+        self.packed_key: Optional[Tuple[object, ...]] = None
 
 
 class UserOptimizedTransformer(BaselineTransformer):
@@ -408,6 +416,8 @@ class UserOptimizedTransformer(BaselineTransformer):
         # graph and lives exactly as long as it (the eager path's workspace is
         # replaced whenever the input shape changes).
         self._cuda_graph_workspace: Optional[torch.Tensor] = None
+        # ... and so does the packed-weight buffer it read at capture
+        self._cuda_graph_packed: Optional[torch.Tensor] = None
         self._cuda_graph_capture_count = 0
         # A captured graph ends at the last block's output; each call applies
         # final_norm from it into a fresh tensor (row mask of the capture).
@@ -467,7 +477,50 @@ class UserOptimizedTransformer(BaselineTransformer):
         if problems:
             raise UnsupportedShapeError("unsupported encoder shape: " + ", ".join(problems))
 
-    def _native_weights(self, device: torch.device) -> Tuple[torch.Tensor, float]:
+    def _pack_sources(self) -> List[torch.Tensor]:
+        """The weights that get tile-packed copies: qkv_proj, out_proj, ffn_in
+        and ffn_out of every layer, in the C ABI's order."""
+        sources: List[torch.Tensor] = []
+        for layer in self.layers:
+            sources += [layer.attention.qkv_proj.weight, layer.attention.out_proj.weight,
+                        layer.ffn_in.weight, layer.ffn_out.weight]
+        return sources
+
+    def _pack_enabled(self, rows: int) -> bool:
+        from . import native
+
+        cfg = self.config
+        d, f = cfg.d_model, cfg.ffn_dim
+        return rows >= PACK_MIN_ROWS and cfg.num_layers > 0 and all(
+            native.prepack_rows(n, k) for n, k in ((3 * d, d), (d, d), (f, d), (d, f)))
+
+    def _packed_weights(self, device: torch.device) -> List[torch.Tensor]:
+        """Tile-packed copies of the projection weights, remade (into the same
+        buffer) whenever a source weight's address or version changes, so an
+        in-place weight update is never served from a stale copy."""
+        from . import native
+
+        sources = self._pack_sources()
+        key = tuple((w.data_ptr(), w._version) for w in sources)
+        state = self._hip
+        if state.packed_key == key and state.packed is not None:
+            return state.packed_views
+        total = sum(w.numel() for w in sources)
+        if state.packed is None or state.packed.numel() != total or state.packed.device != device:
+            state.packed = torch.empty(total, device=device, dtype=torch.bfloat16)
+        views, offset = [], 0
+        for w in sources:
+            view = state.packed[offset:offset + w.numel()]
+            native.prepack_weight(w, out=view)
+            views.append(view)
+            offset += w.numel()  # a multiple of 128 * 32: every view stays 16-byte aligned
+        state.packed_views = views
+        state.packed_key = key
+        return views
+
+    def _native_weights(self, device: torch.device, rows: int = 0) -> Tuple[torch.Tensor, float, bool]:
+        """The C ABI's weight pointer table for an input of ``rows`` tokens,
+        its LayerNorm eps, and whether the table carries packed copies."""
         params: List[torch.Tensor] = []
         eps_values = set()
         for layer in self.layers:
@@ -491,13 +544,16 @@ class UserOptimizedTransformer(BaselineTransformer):
                     "parameters must be contiguous bfloat16 tensors on the input's device"
                 )
         signature = tuple(p.data_ptr() for p in params)
+        packed = self._pack_enabled(rows)
+        if packed:
+            signature += tuple(v.data_ptr() for v in self._packed_weights(device))
         state = self._hip
         if state.weight_signature != signature:
             state.weight_table = torch.tensor(signature, dtype=torch.int64)
             state.weight_signature = signature
             state.eps = float(next(iter(eps_values)))
         assert state.weight_table is not None
-        return state.weight_table, state.eps
+        return state.weight_table, state.eps, packed
 
     def _native_workspace(self, x: torch.Tensor) -> torch.Tensor:
         from . import native
@@ -529,7 +585,7 @@ class UserOptimizedTransformer(BaselineTransformer):
         cfg = self.config
         self._check_native_supported(x)
         x = x.contiguous()
-        table, eps = self._native_weights(x.device)
+        table, eps, packed = self._native_weights(x.device, x.shape[0] * x.shape[1])
         if workspace is None:
             workspace = self._native_workspace(x)
         out = torch.empty_like(x)
@@ -544,7 +600,7 @@ class UserOptimizedTransformer(BaselineTransformer):
         native.encoder_forward(
             x, out, workspace, table, cfg.num_heads, cfg.ffn_dim, cfg.num_layers, eps,
             cfg.causal, kv_len, key_mask, row_mask, online_attention=self.online_attention,
-            final_norm=final_norm,
+            final_norm=final_norm, packed_weights=packed,
         )
         return out
 
@@ -596,6 +652,11 @@ class UserOptimizedTransformer(BaselineTransformer):
                 tuple(valid_token_mask.stride()),
                 valid_token_mask.storage_offset(),
             )
+        # With packed copies in play, an in-place weight update (a new
+        # version) must re-pack them, so it forces a capture.
+        versions: Tuple[int, ...] = ()
+        if self._pack_enabled(x.shape[0] * x.shape[1]):
+            versions = tuple(w._version for w in self._pack_sources())
         return (
             x.untyped_storage().data_ptr(),
             tuple(x.shape),
@@ -605,6 +666,7 @@ class UserOptimizedTransformer(BaselineTransformer):
             mask_kind,
             self.online_attention,
             tuple(p.untyped_storage().data_ptr() for p in self.parameters()),
+            versions,
         )
 
     def _capture_cuda_graph(
@@ -620,6 +682,7 @@ class UserOptimizedTransformer(BaselineTransformer):
         self._cuda_graph_stream = None
         self._cuda_graph_signature = None
         self._cuda_graph_workspace = None
+        self._cuda_graph_packed = None
 
         from . import native
 
@@ -650,6 +713,7 @@ class UserOptimizedTransformer(BaselineTransformer):
         self._cuda_graph = graph
         self._cuda_graph_output = graph_output
         self._cuda_graph_workspace = graph_workspace
+        self._cuda_graph_packed = self._hip.packed
         self._cuda_graph_stream = capture_stream
         self._cuda_graph_signature = signature
         self._cuda_graph_final_norm = True

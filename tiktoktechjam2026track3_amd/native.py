@@ -29,6 +29,7 @@ ENC_ERR_OOM = 4
 
 ENC_FWD_ONLINE_ATTENTION = 1
 ENC_FWD_SKIP_FINAL_NORM = 2
+ENC_FWD_PACKED_WEIGHTS = 4
 
 ENC_EPI_BIAS = 0
 ENC_EPI_BIAS_GELU = 1
@@ -45,6 +46,12 @@ SIGNATURES = (
     ("enc_last_error", ctypes.c_char_p, ()),
     ("enc_layernorm_bf16", ctypes.c_int, (_VP, _VP, _VP, _VP, _I64, _I64, _F32, _VP, _VP)),
     ("enc_linear_bf16", ctypes.c_int, (_VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I32, _VP, _VP)),
+    ("enc_prepack_weight_bf16", ctypes.c_int, (_VP, _VP, _I64, _I64, _VP)),
+    (
+        "enc_linear_prepacked_bf16",
+        ctypes.c_int,
+        (_VP, _VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I32, _VP, _VP),
+    ),
     ("enc_qkv_proj_bf16", ctypes.c_int, (_VP, _VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _VP)),
     (
         "enc_attention_fwd_bf16",
@@ -175,6 +182,31 @@ def layernorm(
     return out
 
 
+def prepack_rows(out_features: int, in_features: int) -> int:
+    """Row-group height of the tile-packed weight layout (256 or 128), or 0
+    when [out_features, in_features] has no packed form (the C ABI's rule)."""
+    if out_features <= 0 or in_features <= 0 or in_features % 32:
+        return 0
+    return 256 if out_features % 256 == 0 else 128 if out_features % 128 == 0 else 0
+
+
+def prepack_weight(weight: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The tile-packed copy of an nn.Linear weight (enc_prepack_weight_bf16),
+    as a flat bf16 tensor of weight.numel() elements."""
+    _require(weight, "weight", torch.bfloat16)
+    n, k = weight.shape
+    if prepack_rows(n, k) == 0:
+        raise ValueError(f"weight {tuple(weight.shape)} has no packed form (out_features % 128, in_features % 32)")
+    out = torch.empty(weight.numel(), device=weight.device, dtype=weight.dtype) if out is None else out
+    if out.numel() != weight.numel() or out.dtype != torch.bfloat16 or not out.is_contiguous():
+        raise ValueError("out must be a contiguous bf16 tensor of weight.numel() elements")
+    _check(
+        "enc_prepack_weight_bf16",
+        load_library().enc_prepack_weight_bf16(weight.data_ptr(), out.data_ptr(), n, k, _stream(weight.device)),
+    )
+    return out
+
+
 def linear(
     a: torch.Tensor,
     weight: torch.Tensor,
@@ -183,8 +215,11 @@ def linear(
     residual: Optional[torch.Tensor] = None,
     row_mask: Optional[torch.Tensor] = None,
     out: Optional[torch.Tensor] = None,
+    packed_weight: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
-    """epilogue(a . weight^T + bias) on MFMA (enc_linear_bf16)."""
+    """epilogue(a . weight^T + bias) on MFMA (enc_linear_bf16; with
+    ``packed_weight``, the prepack_weight copy of weight, through
+    enc_linear_prepacked_bf16)."""
     for tensor, name in ((a, "a"), (weight, "weight"), (bias, "bias")):
         _require(tensor, name, torch.bfloat16)
     n, k = weight.shape
@@ -197,6 +232,18 @@ def linear(
         if residual.shape != out.shape:
             raise ValueError("residual must have the output shape")
     mask = None if row_mask is None else row_mask.contiguous().view(torch.uint8)
+    if packed_weight is not None:
+        _require(packed_weight, "packed_weight", torch.bfloat16)
+        if packed_weight.numel() != weight.numel():
+            raise ValueError("packed_weight must hold weight.numel() elements")
+        _check(
+            "enc_linear_prepacked_bf16",
+            load_library().enc_linear_prepacked_bf16(
+                a.data_ptr(), weight.data_ptr(), packed_weight.data_ptr(), bias.data_ptr(), _ptr(residual),
+                out.data_ptr(), rows, n, k, int(epilogue), _ptr(mask), _stream(a.device),
+            ),
+        )
+        return out
     _check(
         "enc_linear_bf16",
         load_library().enc_linear_bf16(
@@ -312,6 +359,15 @@ def encoder_workspace_bytes(batch: int, seq_len: int, d_model: int, num_heads: i
     return int(size)
 
 
+def _forward_flags(online_attention: bool, final_norm: bool, packed_weights: bool, weight_table: torch.Tensor,
+                   num_layers: int) -> int:
+    expected = 12 * num_layers + 2 + (4 * num_layers if packed_weights else 0)
+    if weight_table.numel() != expected or weight_table.dtype != torch.int64 or weight_table.device.type != "cpu":
+        raise ValueError(f"weight_table must be a CPU int64 tensor of {expected} device pointers")
+    return ((ENC_FWD_ONLINE_ATTENTION if online_attention else 0) | (0 if final_norm else ENC_FWD_SKIP_FINAL_NORM)
+            | (ENC_FWD_PACKED_WEIGHTS if packed_weights else 0))
+
+
 def encoder_forward(
     x: torch.Tensor,
     out: torch.Tensor,
@@ -327,15 +383,18 @@ def encoder_forward(
     row_mask: Optional[torch.Tensor],
     online_attention: bool = False,
     final_norm: bool = True,
+    packed_weights: bool = False,
 ) -> None:
     """Run the whole encoder through enc_encoder_forward_bf16.
 
     ``weight_table`` is a CPU int64 tensor of device pointers in the order the
-    C ABI documents; ``key_mask``/``row_mask`` are uint8 [B, S] tensors.  With
+    C ABI documents (with ``packed_weights``, followed by the packed copies of
+    each layer's four projection weights, ENC_FWD_PACKED_WEIGHTS);
+    ``key_mask``/``row_mask`` are uint8 [B, S] tensors.  With
     ``final_norm=False`` ``out`` receives the last block's output and the
     caller applies final_norm (ENC_FWD_SKIP_FINAL_NORM).
     """
-    flags = (ENC_FWD_ONLINE_ATTENTION if online_attention else 0) | (0 if final_norm else ENC_FWD_SKIP_FINAL_NORM)
+    flags = _forward_flags(online_attention, final_norm, packed_weights, weight_table, num_layers)
     batch, seq_len, d_model = x.shape
     table = ctypes.cast(weight_table.data_ptr(), ctypes.c_void_p)
     _check(
@@ -363,12 +422,13 @@ def encoder_forward_noalloc(
     row_mask: Optional[torch.Tensor],
     online_attention: bool = False,
     final_norm: bool = True,
+    packed_weights: bool = False,
 ) -> None:
     """enc_encoder_forward_bf16_noalloc: the encoder forward over the library's
     own static scratch array (no workspace argument, no device allocation).
     Calls that overlap on one GPU share that array and must not run
     concurrently."""
-    flags = (ENC_FWD_ONLINE_ATTENTION if online_attention else 0) | (0 if final_norm else ENC_FWD_SKIP_FINAL_NORM)
+    flags = _forward_flags(online_attention, final_norm, packed_weights, weight_table, num_layers)
     batch, seq_len, d_model = x.shape
     table = ctypes.cast(weight_table.data_ptr(), ctypes.c_void_p)
     _check(
