@@ -105,6 +105,24 @@ int enc_linear_prepacked_bf16(const void* a, const void* weight,
                               int32_t epilogue, const uint8_t* row_mask,
                               void* stream);
 
+/* The FFN half of an encoder block in one call, as the reference's block
+ * computes it (models.py:724-725, 734-737):
+ *   hidden = bf16(gelu_erf(bf16(h . w_in^T + b_in)))       [rows, ffn_dim]
+ *   out    = bf16(residual + bf16(hidden . w_out^T + b_out)) [rows, d_model]
+ * and, with row_mask non-null, out rows with row_mask[r] == 0 are zeros (the
+ * block output's masked_fill).  Two MFMA GEMM launches with the GELU and the
+ * residual fused into their epilogues; hidden is caller workspace of
+ * rows * ffn_dim bf16 that must not overlap h, residual or out (out may
+ * alias residual).  d_model and ffn_dim multiples of 32.  Bitwise the
+ * encoder forward's FFN.  Replaces ffn_in / F.gelu / ffn_out + residual at
+ * models.py:724-725, 734 and the candidate's fused wrappers fused_ffn.py:91-126
+ * and fused_ffn_out.py:89-132. */
+int enc_ffn_fused_bf16(const void* h, const void* w_in, const void* b_in,
+                       const void* w_out, const void* b_out,
+                       const void* residual, void* out, void* hidden,
+                       int64_t rows, int64_t d_model, int64_t ffn_dim,
+                       const uint8_t* row_mask, void* stream);
+
 /* Packed QKV projection x[batch*seq_len, d_model] . qkv_weight[3*d_model,
  * d_model]^T + qkv_bias, rounded to bf16 and written head-major:
  *   q, k : [batch, num_heads, seq_len, head_dim]

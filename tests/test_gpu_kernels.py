@@ -299,6 +299,36 @@ def test_linear_prepacked_rejects_unpackable_shapes(device):
     assert info.value.code == native.ENC_ERR_UNSUPPORTED
 
 
+@pytest.mark.parametrize("rows,d,f", [(128, 512, 2048), (8192, 1024, 4096), (100000, 1024, 1024), (4096, 128, 128),
+                                     (300, 256, 1024)])
+def test_ffn_fused_is_the_reference_ffn(device, rows, d, f):
+    """enc_ffn_fused_bf16 = residual + ffn_out(gelu(ffn_in(h))) with the
+    block's masked rows zeroed, bit for bit as torch computes the reference
+    block's FFN (models.py:724-725, 734-737)."""
+    g = torch.Generator(device=device).manual_seed(rows + d + f)
+    h = torch.randn(rows, d, generator=g, device=device).bfloat16()
+    res = torch.randn(rows, d, generator=g, device=device).bfloat16()
+    w1 = ((torch.rand(f, d, generator=g, device=device) * 2 - 1) / math.sqrt(d)).bfloat16()
+    b1 = ((torch.rand(f, generator=g, device=device) * 2 - 1) / math.sqrt(d)).bfloat16()
+    w2 = ((torch.rand(d, f, generator=g, device=device) * 2 - 1) / math.sqrt(f)).bfloat16()
+    b2 = ((torch.rand(d, generator=g, device=device) * 2 - 1) / math.sqrt(f)).bfloat16()
+    mask = torch.rand(rows, generator=g, device=device) > 0.2
+    out = native.ffn(h, w1, b1, w2, b2, res, row_mask=mask)
+    ref = res + F.linear(F.gelu(F.linear(h, w1, b1), approximate="none"), w2, b2)
+    ref = ref.masked_fill(~mask[:, None], 0)
+    mismatches = int((ref.view(torch.int16) != out.view(torch.int16)).sum())
+    print(f"[ffn] {rows}x{d}x{f}: {mismatches} mismatches against torch", flush=True)
+    assert mismatches == 0
+    # the same two products through enc_linear_bf16
+    two = native.linear(native.linear(h, w1, b1, native.ENC_EPI_BIAS_GELU), w2, b2,
+                        native.ENC_EPI_BIAS_RESIDUAL_ZERO, residual=res, row_mask=mask)
+    assert torch.equal(two, out)
+    # out may alias the residual
+    inplace = res.clone()
+    native.ffn(h, w1, b1, w2, b2, inplace, row_mask=mask, out=inplace)
+    assert torch.equal(inplace, out)
+
+
 @pytest.mark.parametrize(
     "b,s,d,h",
     [(1, 128, 512, 8), (2, 100, 512, 8), (8, 1024, 1024, 16), (3, 37, 1024, 16), (64, 128, 32, 4), (3, 37, 128, 16),

@@ -318,3 +318,17 @@ def test_encoder_packed_flag_needs_the_packed_pointers():
     assert rc == native.ENC_ERR_UNSUPPORTED and b"packed weights" in lib.enc_last_error()
     with pytest.raises(ValueError, match="18 device pointers"):
         native._forward_flags(False, True, True, torch.zeros(14, dtype=torch.int64), 1)
+
+
+def test_ffn_entry_point_checks_arguments_before_any_device_call():
+    lib = native.load_library()
+    p = [ctypes.c_void_p(4096 * (i + 1)) for i in range(7)]
+    hidden = ctypes.c_void_p(1 << 30)
+    rc = lib.enc_ffn_fused_bf16(*p[:7], hidden, 128, 512, 2000, None, None)
+    assert rc == native.ENC_ERR_UNSUPPORTED and b"multiples of 32" in lib.enc_last_error()
+    rc = lib.enc_ffn_fused_bf16(*p[:6], None, hidden, 128, 512, 2048, None, None)
+    assert rc == native.ENC_ERR_INVALID and b"null" in lib.enc_last_error()
+    # hidden overlapping the input rows (h at 4096, 128 x 512 bf16 = 128 KiB)
+    rc = lib.enc_ffn_fused_bf16(*p[:7], ctypes.c_void_p(4096 + 1024), 128, 512, 2048, None, None)
+    assert rc == native.ENC_ERR_INVALID and b"overlap" in lib.enc_last_error()
+    assert lib.enc_ffn_fused_bf16(*p[:7], hidden, 0, 512, 2048, None, None) == native.ENC_OK

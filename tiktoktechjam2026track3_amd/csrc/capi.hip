@@ -23,8 +23,8 @@ int fail(int code, const std::string& msg) {
   return code;
 }
 
-int fail_hip(hipError_t err, const char* where) {
-  std::string msg = std::string(where) + ": " + hipGetErrorString(err);
+int fail_hip(hipError_t err, const std::string& where) {
+  std::string msg = where + ": " + hipGetErrorString(err);
   if (err == hipErrorOutOfMemory || err == hipErrorMemoryAllocation) {
     return fail(ENC_ERR_OOM, msg + " (out of memory)");
   }
@@ -169,6 +169,38 @@ int check_encoder_call(const void* x, void* out, const void* const* weights, int
   return ENC_OK;
 }
 
+// The FFN half of a block: hidden = bf16(gelu(bf16(h . w_in^T + b_in))),
+// out = bf16(residual + bf16(hidden . w_out^T + b_out)), rows with
+// row_mask == 0 written as zeros (the block output's masked_fill).  Optional
+// packed weight copies (null: the plain weights only).
+hipError_t ffn_block(const enc::bf16_t* h, const enc::bf16_t* w_in, const enc::bf16_t* b_in,
+                     const enc::bf16_t* w_out, const enc::bf16_t* b_out, const enc::bf16_t* residual,
+                     enc::bf16_t* out, enc::bf16_t* hidden, int64_t rows, int64_t D, int64_t F,
+                     const uint8_t* row_mask, const enc::bf16_t* w_in_packed, const enc::bf16_t* w_out_packed,
+                     int cus, hipStream_t st, const char** stage) {
+  enc::GemmEpilogueArgs fa;
+  fa.bias = b_in;
+  fa.out = hidden;
+  if (w_in_packed) {
+    fa.w_packed = w_in_packed;
+    fa.w_packed_rows = enc::gemm_prepack_rows(F, D);
+  }
+  *stage = "ffn_in";
+  hipError_t e = enc::gemm_bf16(h, w_in, rows, F, D, enc::kEpiBiasGelu, fa, cus, st);
+  if (e != hipSuccess) return e;
+  enc::GemmEpilogueArgs fo;
+  fo.bias = b_out;
+  fo.residual = residual;
+  fo.row_mask = row_mask;
+  fo.out = out;
+  if (w_out_packed) {
+    fo.w_packed = w_out_packed;
+    fo.w_packed_rows = enc::gemm_prepack_rows(D, F);
+  }
+  *stage = "ffn_out";
+  return enc::gemm_bf16(hidden, w_out, rows, D, F, enc::kEpiResidualZero, fo, cus, st);
+}
+
 // The launch sequence of the encoder forward over a workspace laid out as `w`.
 int run_encoder_forward(const void* x, void* out, void* workspace, const EncoderWorkspace& w,
                         const void* const* weights, int64_t batch, int64_t seq_len, int64_t d_model,
@@ -197,9 +229,12 @@ int run_encoder_forward(const void* x, void* out, void* workspace, const Encoder
   // Tile-packed copies of the four projection weights (qkv, out, ffn_in,
   // ffn_out) follow the 12 * num_layers + 2 pointers when asked for.
   const bool packed = (flags & ENC_FWD_PACKED_WEIGHTS) != 0;
+  auto P = [&](int64_t layer, int which) {
+    return static_cast<const bf16_t*>(weights[12 * num_layers + 2 + 4 * layer + which]);
+  };
   auto use_packed = [&](enc::GemmEpilogueArgs& a, int64_t layer, int which, int64_t n, int64_t k) {
     if (!packed) return;
-    a.w_packed = static_cast<const bf16_t*>(weights[12 * num_layers + 2 + 4 * layer + which]);
+    a.w_packed = P(layer, which);
     a.w_packed_rows = enc::gemm_prepack_rows(n, k);
   };
 
@@ -281,23 +316,13 @@ int run_encoder_forward(const void* x, void* out, void* workspace, const Encoder
     // norm2
     e = enc::layernorm_bf16(x_attn, W(layer, 6), W(layer, 7), ln, T, D, eps, nullptr, st);
     if (e != hipSuccess) return fail_hip(e, "encoder norm2");
-    // ffn_in + exact GELU
-    enc::GemmEpilogueArgs fa;
-    fa.bias = W(layer, 9);
-    fa.out = hidden;
-    use_packed(fa, layer, 2, F, D);
-    e = enc::gemm_bf16(ln, W(layer, 8), T, F, D, enc::kEpiBiasGelu, fa, cus, st);
-    if (e != hipSuccess) return fail_hip(e, "encoder ffn_in");
-    // ffn_out + residual; padded rows are zeroed (block output masked_fill)
+    // ffn_in + exact GELU, then ffn_out + residual; padded rows are zeroed
+    // (block output masked_fill)
     bf16_t* x_next = (!final_norm && layer == num_layers - 1) ? static_cast<bf16_t*>(out) : (x_attn == xa) ? xb : xa;
-    enc::GemmEpilogueArgs fo;
-    fo.bias = W(layer, 11);
-    fo.residual = x_attn;
-    fo.row_mask = row_mask;
-    fo.out = x_next;
-    use_packed(fo, layer, 3, D, F);
-    e = enc::gemm_bf16(hidden, W(layer, 10), T, D, F, enc::kEpiResidualZero, fo, cus, st);
-    if (e != hipSuccess) return fail_hip(e, "encoder ffn_out");
+    const char* stage = "";
+    e = ffn_block(ln, W(layer, 8), W(layer, 9), W(layer, 10), W(layer, 11), x_attn, x_next, hidden, T, D, F, row_mask,
+                  packed ? P(layer, 2) : nullptr, packed ? P(layer, 3) : nullptr, cus, st, &stage);
+    if (e != hipSuccess) return fail_hip(e, std::string("encoder ") + stage);
     cur = x_next;
   }
   if (!final_norm) return ok();  // out holds the last block's output
@@ -404,6 +429,36 @@ int enc_linear_prepacked_bf16(const void* a, const void* weight, const void* pac
   if (!packed_weight) return fail(ENC_ERR_INVALID, "linear: null packed weight");
   return linear_entry(a, weight, packed_weight, bias, residual, out, rows, out_features, in_features, epilogue,
                       row_mask, stream);
+}
+
+int enc_ffn_fused_bf16(const void* h, const void* w_in, const void* b_in, const void* w_out, const void* b_out,
+                       const void* residual, void* out, void* hidden, int64_t rows, int64_t d_model,
+                       int64_t ffn_dim, const uint8_t* row_mask, void* stream) {
+  if (rows < 0 || d_model <= 0 || ffn_dim <= 0) return fail(ENC_ERR_INVALID, "ffn: rows must be >= 0, widths > 0");
+  if (rows == 0) return ok();
+  if (!h || !w_in || !b_in || !w_out || !b_out || !residual || !out || !hidden)
+    return fail(ENC_ERR_INVALID, "ffn: null tensor pointer");
+  if (!enc::gemm_supported(rows, ffn_dim, d_model) || !enc::gemm_supported(rows, d_model, ffn_dim))
+    return fail(ENC_ERR_UNSUPPORTED, "ffn: d_model and ffn_dim must be multiples of 32 (got " +
+                                         std::to_string(d_model) + ", " + std::to_string(ffn_dim) + ")");
+  // hidden is written by the first product and read by the second
+  auto span_overlaps = [](const void* a, int64_t a_bytes, const void* b, int64_t b_bytes) {
+    const char* pa = static_cast<const char*>(a);
+    const char* pb = static_cast<const char*>(b);
+    return pa < pb + b_bytes && pb < pa + a_bytes;
+  };
+  const int64_t hidden_bytes = rows * ffn_dim * 2, act_bytes = rows * d_model * 2;
+  if (span_overlaps(hidden, hidden_bytes, h, act_bytes) || span_overlaps(hidden, hidden_bytes, out, act_bytes) ||
+      span_overlaps(hidden, hidden_bytes, residual, act_bytes))
+    return fail(ENC_ERR_INVALID, "ffn: hidden must not overlap h, residual or out");
+  const char* stage = "";
+  hipError_t e = ffn_block(static_cast<const enc::bf16_t*>(h), static_cast<const enc::bf16_t*>(w_in),
+                           static_cast<const enc::bf16_t*>(b_in), static_cast<const enc::bf16_t*>(w_out),
+                           static_cast<const enc::bf16_t*>(b_out), static_cast<const enc::bf16_t*>(residual),
+                           static_cast<enc::bf16_t*>(out), static_cast<enc::bf16_t*>(hidden), rows, d_model, ffn_dim,
+                           row_mask, nullptr, nullptr, device_cus(), static_cast<hipStream_t>(stream), &stage);
+  if (e != hipSuccess) return fail_hip(e, std::string("ffn ") + stage);
+  return ok();
 }
 
 int enc_qkv_proj_bf16(const void* x, const void* weight, const void* bias, void* q, void* k, void* v_t,

@@ -52,6 +52,7 @@ SIGNATURES = (
         ctypes.c_int,
         (_VP, _VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I32, _VP, _VP),
     ),
+    ("enc_ffn_fused_bf16", ctypes.c_int, (_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _VP, _VP)),
     ("enc_qkv_proj_bf16", ctypes.c_int, (_VP, _VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _VP)),
     (
         "enc_attention_fwd_bf16",
@@ -249,6 +250,43 @@ def linear(
         load_library().enc_linear_bf16(
             a.data_ptr(), weight.data_ptr(), bias.data_ptr(), _ptr(residual), out.data_ptr(),
             rows, n, k, int(epilogue), _ptr(mask), _stream(a.device),
+        ),
+    )
+    return out
+
+
+def ffn(
+    h: torch.Tensor,
+    w_in: torch.Tensor,
+    b_in: torch.Tensor,
+    w_out: torch.Tensor,
+    b_out: torch.Tensor,
+    residual: torch.Tensor,
+    row_mask: Optional[torch.Tensor] = None,
+    out: Optional[torch.Tensor] = None,
+    hidden: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """residual + ffn_out(gelu(ffn_in(h))), masked rows zeroed
+    (enc_ffn_fused_bf16); ``hidden`` is the [rows, ffn_dim] workspace."""
+    for tensor, name in ((h, "h"), (w_in, "w_in"), (b_in, "b_in"), (w_out, "w_out"), (b_out, "b_out"),
+                         (residual, "residual")):
+        _require(tensor, name, torch.bfloat16)
+    f, d = w_in.shape
+    if h.shape[-1] != d or tuple(w_out.shape) != (d, f) or b_in.numel() != f or b_out.numel() != d:
+        raise ValueError(f"shape mismatch: h {tuple(h.shape)}, w_in {tuple(w_in.shape)}, w_out {tuple(w_out.shape)}")
+    if residual.shape != h.shape:
+        raise ValueError("residual must have h's shape")
+    rows = h.numel() // d
+    out = torch.empty_like(h) if out is None else out
+    hidden = torch.empty((rows, f), device=h.device, dtype=h.dtype) if hidden is None else hidden
+    if hidden.numel() < rows * f or not hidden.is_contiguous():
+        raise ValueError("hidden must be a contiguous workspace of rows * ffn_dim elements")
+    mask = None if row_mask is None else row_mask.contiguous().view(torch.uint8)
+    _check(
+        "enc_ffn_fused_bf16",
+        load_library().enc_ffn_fused_bf16(
+            h.data_ptr(), w_in.data_ptr(), b_in.data_ptr(), w_out.data_ptr(), b_out.data_ptr(),
+            residual.data_ptr(), out.data_ptr(), hidden.data_ptr(), rows, d, f, _ptr(mask), _stream(h.device),
         ),
     )
     return out
