@@ -6,7 +6,8 @@ must leave enough wait states (independent instructions, or ``s_nop``) between
 the MFMA and the first instruction that reads its result.  The compiler
 inserts them, but a branch between the MFMA and the read once let a read on
 the branch-taken path follow after two instructions (a nondeterministic wrong
-result, see DESIGN notes in the repository).  This module disassembles the
+result in the last result register of the fused block tail's products).  This
+module disassembles the
 device code of every object the build produced and walks each MFMA's
 successors along every control-flow path, counting wait states, and reports
 each read of the MFMA's destination that comes too early.
