@@ -110,6 +110,31 @@ def test_encoder_parity_narrow_ragged(device, cfg):
             assert torch.equal(ref, out)
 
 
+@pytest.mark.parametrize(
+    "cfg",
+    [TransformerConfig(1, 100, 256, 4, 512, 3, True), TransformerConfig(2, 64, 512, 8, 1024, 2, False),
+     TransformerConfig(1, 256, 1024, 16, 1024, 2, True), TransformerConfig(3, 50, 2048, 16, 512, 2, False)],
+    ids=["d256-ragged-causal", "d512", "d1024-256rows-causal", "d2048"],
+)
+def test_encoder_parity_few_row_models(device, cfg):
+    """Up to 256 tokens with d_model 256-2048 every projection takes the
+    few-row (16-row tile) kernels, split-K where the library splits: bit for
+    bit the oracle, with and without padding (a partial last row block at 100
+    and 150 tokens), on the capturing call and on two graph replays."""
+    sd, candidate = build_models(cfg, 91, device)
+    for padding in (0.0, 0.3):
+        with torch.inference_mode():
+            x, mask = generate_random_case(cfg, device, torch.bfloat16, 7, padding, 1.0)
+            outs = [candidate(x, mask) for _ in range(3)]
+            ref = encoder_forward(sd, x, mask, cfg.causal, cfg.num_heads, cfg.num_layers)
+            torch.cuda.synchronize()
+        result = compare(ref, outs[0], RTOL, ATOL)
+        print(f"[parity] few-row model {cfg} padding {padding}: {result}", flush=True)
+        assert result["passed"], result
+        for out in outs:
+            assert torch.equal(ref, out)
+
+
 def test_encoder_parity_second_trial_c4(device):
     result, _, _ = run_parity("c4", device, trial=1)
     assert result["passed"], result
