@@ -160,6 +160,27 @@ def test_linear_gelu(device, m, n, k):
     assert bitwise_fraction(F.gelu(F.linear(a, w, bias), approximate="none"), out) > 0.999
 
 
+@pytest.mark.parametrize("packed", [False, True], ids=["plain", "packed"])
+def test_gelu_epilogue_every_bf16_input(device, packed):
+    """The wide kernel's GELU epilogue looks its result up in a table of
+    bf16(gelu_erf(x)) over all 65536 bf16 patterns x, filled on the device by
+    the same erf code.  With zero weights the nn.Linear output is the bias
+    (+0 for a -0 bias, NaN for a NaN one), so a bias row holding every bf16
+    pattern sends each table entry through the epilogue: bit for bit torch's
+    GELU of torch's product, NaN for NaN, on every row."""
+    m, n, k = 1024, 65536, 64
+    a = torch.randn(m, k, device=device).bfloat16()
+    w = torch.zeros(n, k, device=device, dtype=torch.bfloat16)
+    bias = torch.arange(n, device=device, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    wp = native.prepack_weight(w) if packed else None
+    out = native.linear(a, w, bias, native.ENC_EPI_BIAS_GELU, packed_weight=wp)
+    ref = F.gelu(F.linear(a, w, bias), approximate="none")
+    nan_out, nan_ref = torch.isnan(out), torch.isnan(ref)
+    assert torch.equal(nan_out, nan_ref)
+    same = out.view(torch.int16) == ref.view(torch.int16)
+    assert bool((same | nan_ref).all()), int((~(same | nan_ref)).sum())
+
+
 @pytest.mark.parametrize("epi", [native.ENC_EPI_BIAS_RESIDUAL_KEEP, native.ENC_EPI_BIAS_RESIDUAL_ZERO])
 @pytest.mark.parametrize("m,n,k", [(100, 512, 512), (8192, 1024, 1024), (1000, 1024, 4096)])
 def test_linear_residual(device, m, n, k, epi):

@@ -22,6 +22,8 @@
 // workgroups round-robin over its 8 XCDs, so the linear id is remapped so each
 // XCD walks a contiguous range of tiles, which are ordered in groups of 8 tile
 // rows so concurrently running tiles share A rows and W columns in that XCD's L2.
+#include <mutex>
+
 #include "common.h"
 #include "kernels.h"
 #include "streamk_tail.h"
@@ -53,6 +55,17 @@ __device__ __forceinline__ void map_tile(int tiles_m, int tiles_n, int pid, int*
   const int in_group = pid % per_group;
   *tm = first_m + in_group % group_m;
   *tn = in_group / group_m;
+}
+
+// torch's exact GELU of every bf16 value, bf16(gelu_erf(x)) for all 65536 bit
+// patterns x, filled on each device by gelu_table_kernel before its first GELU
+// product: the input of a GELU epilogue is the bf16 nn.Linear output, so one
+// lookup gives the same bits as the erf evaluation.
+__device__ __attribute__((aligned(256))) uint16_t g_gelu_table[65536];
+
+__global__ void __launch_bounds__(256) gelu_table_kernel() {
+  const uint32_t x = blockIdx.x * 256u + threadIdx.x;
+  g_gelu_table[x] = f32_to_bf16(gelu_erf(__uint_as_float(x << 16)));
 }
 
 template <int EPI>
@@ -391,10 +404,11 @@ __device__ __forceinline__ void finish8(const GemmEpilogueArgs& ep, int N, int r
   if constexpr (EPI == kEpiBias) {
     w = u32x4{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]), pack_bf16x2(y[4], y[5]), pack_bf16x2(y[6], y[7])};
   } else if constexpr (EPI == kEpiBiasGelu) {
-    float g[8];
+    // y holds bf16 values: the table lookup is the erf GELU of each
+    uint32_t g[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) g[e] = gelu_erf(y[e]);
-    w = u32x4{pack_bf16x2(g[0], g[1]), pack_bf16x2(g[2], g[3]), pack_bf16x2(g[4], g[5]), pack_bf16x2(g[6], g[7])};
+    for (int e = 0; e < 8; ++e) g[e] = g_gelu_table[__float_as_uint(y[e]) >> 16];
+    w = u32x4{g[0] | (g[1] << 16), g[2] | (g[3] << 16), g[4] | (g[5] << 16), g[6] | (g[7] << 16)};
   } else {
     if (keep) {
       float o[8];
@@ -1017,9 +1031,39 @@ hipError_t launch_split(const bf16_t* A, const bf16_t* W, int M, int N, int K, i
   return hipGetLastError();
 }
 
+// Fills g_gelu_table on the current device before its first GELU product.
+// The fill runs on the caller's stream, which is then synchronised once, so
+// products on other streams find the table complete; inside a stream capture
+// the fill is recorded into the graph instead (stream order covers the
+// graph's products) and the device stays unmarked.
+std::mutex g_gelu_mutex;
+bool g_gelu_ready[64] = {false};
+
+hipError_t ensure_gelu_table(hipStream_t st) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> guard(g_gelu_mutex);
+  if (g_gelu_ready[dev]) return hipSuccess;
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  e = hipStreamIsCapturing(st, &capture);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(gelu_table_kernel, dim3(256), dim3(256), 0, st);
+  e = hipGetLastError();
+  if (e != hipSuccess || capture != hipStreamCaptureStatusNone) return e;
+  e = hipStreamSynchronize(st);
+  if (e == hipSuccess) g_gelu_ready[dev] = true;
+  return e;
+}
+
 template <int BM, int BN, int BK, int NS, int OCC = 1>
 hipError_t launch_big(const bf16_t* A, const bf16_t* W, int M, int N, int K, int epi,
                       const GemmEpilogueArgs& ep, hipStream_t st) {
+  if (epi == kEpiBiasGelu) {
+    const hipError_t e = ensure_gelu_table(st);
+    if (e != hipSuccess) return e;
+  }
   const int tiles = ((M + BM - 1) / BM) * (N / BN);
   const dim3 grid(tiles), block(kThreads);
   switch (epi) {
