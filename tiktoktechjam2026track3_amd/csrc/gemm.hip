@@ -28,6 +28,14 @@
 #include "kernels.h"
 #include "streamk_tail.h"
 
+// Raw buffer load into LDS (the LLVM intrinsic, bound by name): byte address =
+// resource base + soffset + voffset; the LDS destination is the instruction's
+// uniform base (M0) plus 16 bytes per lane.
+typedef int32_t enc_rsrc_t __attribute__((ext_vector_type(4)));
+__device__ void enc_buffer_load_lds(enc_rsrc_t rsrc, __attribute__((address_space(3))) uint32_t* lds, int size,
+                                    int voffset, int soffset, int offset, int aux)
+    __asm("llvm.amdgcn.raw.buffer.load.lds");
+
 namespace enc {
 
 namespace {
@@ -335,9 +343,9 @@ gemm_narrow_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, i
 // wavefronts in a 2 x 2 grid, each owning a (BM/2) x (BN/2) sub-tile of 32x32
 // fp32 accumulator blocks (up to 256 registers per lane, held in AGPRs).
 //
-// Operands move global -> LDS with global_load_lds_dwordx4, without register
-// staging: one instruction writes 64 consecutive 16-byte LDS chunks, one per
-// lane, so the LDS layout is chosen on the global side.  An LDS row holds one
+// Operands move global -> LDS with buffer_load_dwordx4 ... lds, without
+// register staging: one instruction writes 64 consecutive 16-byte LDS chunks,
+// one per lane, so the LDS layout is chosen on the global side.  An LDS row holds one
 // A or W row of the BK-wide K slice as BK/8 chunks of 8 bf16, chunk c stored
 // in slot c ^ swz(row) (swz = row & 7 for 8 chunks a row, (row >> 1) & 3 for
 // 4), so the 32 rows one MFMA fragment read touches at one K chunk land in
@@ -373,6 +381,15 @@ __device__ __forceinline__ void interleave() {
     for (int l = q * kLoadsPer; l < (q + 1) * kLoadsPer && l < LOADS; ++l)
       __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // global load
   }
+}
+
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+// Buffer resource over [p, p + 4 GiB): stride 0, no range limit, the gfx9
+// raw-buffer format word.  The loads below stay inside their tile's rows.
+__device__ __forceinline__ i32x4 buffer_rsrc(const void* p) {
+  const uint64_t a = reinterpret_cast<uint64_t>(p);
+  return i32x4{static_cast<int32_t>(static_cast<uint32_t>(a)),
+               static_cast<int32_t>(static_cast<uint32_t>(a >> 32) & 0xffffu), -1, 0x00020000};
 }
 
 template <int BM, int BN, int BK, int NS>
@@ -454,9 +471,9 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
   // first row (32-bit); the bases are uniform.
   const int lrow = lane / T::kChunks;
   const int gcol = ((lane % T::kChunks) ^ T::swz(lrow)) * 8;
-  // Each load instruction reads [uniform base + per-lane 32-bit byte offset];
-  // the offsets do not change along K (the compiler hoists them), only the
-  // bases do.  (They are not precomputed into an array: a local array
+  // Each load instruction reads [tile base + uniform K offset + per-lane 32-bit
+  // byte offset]; the per-lane offsets do not change along K (the compiler
+  // hoists them).  (They are not precomputed into an array: a local array
   // captured by the loading lambda makes clang's host pass drop the kernel's
   // launch stub.)
   const char* a_tile = reinterpret_cast<const char*>(A + static_cast<int64_t>(m0) * K);
@@ -471,6 +488,13 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
   const char* w_tile = w_packed ? reinterpret_cast<const char*>(ep.w_packed + static_cast<int64_t>(n0 - n0 % pn) * K)
                                 : reinterpret_cast<const char*>(W + static_cast<int64_t>(n0) * K);
   const int w_k_mul = w_packed ? pn : 1;  // element step of W per unit of k0
+  // The ring loads are buffer loads on per-tile resources: a lane's operand is
+  // a 32-bit offset (hoisted out of the K loop) and the K step a uniform
+  // soffset.  With 64-bit per-lane addresses (global_load_lds) the same loads
+  // took more issue time away from the MFMAs: 1-4% slower on every wide
+  // product, same bits.
+  const i32x4 a_rsrc = buffer_rsrc(a_tile);
+  const i32x4 w_rsrc = buffer_rsrc(w_tile);
   const int w_row0 = w_packed ? n0 % pn : 0;
 
   f32x16 acc[RM][RN];
@@ -513,8 +537,10 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
           is_a ? static_cast<uint32_t>(min(row + lrow, a_rows_left) * K + gcol) * 2u
           : w_packed ? static_cast<uint32_t>((gcol >> 5) * pn * 32 + (w_row0 + row + lrow) * 32 + (gcol & 31)) * 2u
                      : static_cast<uint32_t>((row + lrow) * K + gcol) * 2u;
-      __builtin_amdgcn_global_load_lds((is_a ? a_tile + 2 * k0 : w_tile + 2 * k0 * w_k_mul) + off,
-                                       sa + (is_a ? 0 : BM * BK) + row * BK, 16, 0, 0);
+      enc_buffer_load_lds(is_a ? a_rsrc : w_rsrc,
+                      reinterpret_cast<__attribute__((address_space(3))) uint32_t*>(
+                          reinterpret_cast<uintptr_t>(sa + (is_a ? 0 : BM * BK) + row * BK)),
+                      16, static_cast<int>(off), is_a ? 2 * k0 : 2 * k0 * w_k_mul, 0, 0);
     }
   };
   // Wait until at most n of this thread's load instructions are in flight and
