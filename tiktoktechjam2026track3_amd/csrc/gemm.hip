@@ -66,15 +66,25 @@ __device__ __forceinline__ void map_tile(int tiles_m, int tiles_n, int pid, int*
 }
 
 // torch's exact GELU of every bf16 value, bf16(gelu_erf(x)) for all 65536 bit
-// patterns x, filled on each device by gelu_table_kernel before its first GELU
-// product: the input of a GELU epilogue is the bf16 nn.Linear output, so one
-// lookup gives the same bits as the erf evaluation.
+// patterns x: the input of a GELU epilogue is the bf16 nn.Linear output, so
+// one lookup gives the same bits as the erf evaluation.  Each device's table
+// is filled by gelu_table_kernel, after which gelu_ready_kernel sets
+// g_gelu_ready on the same stream; an epilogue that finds the flag clear
+// (a product on another stream racing the first fill, or a cached copy of
+// the flag from before it was set) evaluates the erf instead, which gives the
+// same bits.
 __device__ __attribute__((aligned(256))) uint16_t g_gelu_table[65536];
+__device__ uint32_t g_gelu_ready;
 
 __global__ void __launch_bounds__(256) gelu_table_kernel() {
   const uint32_t x = blockIdx.x * 256u + threadIdx.x;
   g_gelu_table[x] = f32_to_bf16(gelu_erf(__uint_as_float(x << 16)));
 }
+
+__global__ void gelu_ready_kernel() {
+  __hip_atomic_store(&g_gelu_ready, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 
 template <int EPI>
 __device__ __forceinline__ void store_row_major(const GemmEpilogueArgs& ep, int N, int row,
@@ -415,17 +425,24 @@ struct BigTile {
 template <int EPI>
 __device__ __forceinline__ void finish8(const GemmEpilogueArgs& ep, int N, int row, int col,
                                         const float (&y)[8], u32x4 r = u32x4{0u, 0u, 0u, 0u},
-                                        bool keep = true) {
+                                        bool keep = true, bool gelu_table = false) {
   const int64_t idx = static_cast<int64_t>(row) * N + col;
   u32x4 w;
   if constexpr (EPI == kEpiBias) {
     w = u32x4{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]), pack_bf16x2(y[4], y[5]), pack_bf16x2(y[6], y[7])};
   } else if constexpr (EPI == kEpiBiasGelu) {
-    // y holds bf16 values: the table lookup is the erf GELU of each
-    uint32_t g[8];
+    if (gelu_table) {
+      // y holds bf16 values: the table lookup is the erf GELU of each
+      uint32_t g[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) g[e] = g_gelu_table[__float_as_uint(y[e]) >> 16];
-    w = u32x4{g[0] | (g[1] << 16), g[2] | (g[3] << 16), g[4] | (g[5] << 16), g[6] | (g[7] << 16)};
+      for (int e = 0; e < 8; ++e) g[e] = g_gelu_table[__float_as_uint(y[e]) >> 16];
+      w = u32x4{g[0] | (g[1] << 16), g[2] | (g[3] << 16), g[4] | (g[5] << 16), g[6] | (g[7] << 16)};
+    } else {
+      float g[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) g[e] = gelu_erf(y[e]);
+      w = u32x4{pack_bf16x2(g[0], g[1]), pack_bf16x2(g[2], g[3]), pack_bf16x2(g[4], g[5]), pack_bf16x2(g[6], g[7])};
+    }
   } else {
     if (keep) {
       float o[8];
@@ -464,6 +481,10 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
   const int wn = wave & 1;
   const int l32 = lane & 31;
   const int lhi = lane >> 5;
+  // the GELU table's ready flag, read now so that its latency hides behind
+  // the K loop (a plain load: a stale 0 only selects the erf)
+  uint32_t gelu_flag = 0u;
+  if constexpr (EPI == kEpiBiasGelu) gelu_flag = g_gelu_ready;
 
   // Load instruction j of wavefront w fills LDS rows R (4 j + w) .. + R - 1
   // (R = rows per instruction); lane -> row + lane / chunks, slot lane % chunks,
@@ -697,23 +718,33 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
   __syncthreads();
 
   if constexpr (EPI != kEpiQkvHeadMajor) {
+    // one verdict per wavefront (the flag only ever turns on)
+    // the passes, with the GELU's table (or erf) fixed for the whole loop
+    auto passes = [&](bool gelu_table) __attribute__((always_inline)) {
 #pragma unroll
-    for (int p = 0; p < kPasses; ++p) {
-      const int rl = rl0 + p * kRowsPerPass;
-      const int row = m0 + rl;
-      if (row < M) {
-        const u32x4 v = *reinterpret_cast<const u32x4*>(sc + rl * T::kLdc + c8);
-        const float y[8] = {lo_bf16(v[0]), hi_bf16(v[0]), lo_bf16(v[1]), hi_bf16(v[1]),
-                            lo_bf16(v[2]), hi_bf16(v[2]), lo_bf16(v[3]), hi_bf16(v[3])};
+      for (int p = 0; p < kPasses; ++p) {
+        const int rl = rl0 + p * kRowsPerPass;
+        const int row = m0 + rl;
+        if (row < M) {
+          const u32x4 v = *reinterpret_cast<const u32x4*>(sc + rl * T::kLdc + c8);
+          const float y[8] = {lo_bf16(v[0]), hi_bf16(v[0]), lo_bf16(v[1]), hi_bf16(v[1]),
+                              lo_bf16(v[2]), hi_bf16(v[2]), lo_bf16(v[3]), hi_bf16(v[3])};
+          if constexpr (kResidual) {
+            finish8<EPI>(ep, N, row, n0 + c8, y, res[p % kDepth], keep[p % kDepth]);
+          } else {
+            finish8<EPI>(ep, N, row, n0 + c8, y, u32x4{0u, 0u, 0u, 0u}, true, gelu_table);
+          }
+        }
         if constexpr (kResidual) {
-          finish8<EPI>(ep, N, row, n0 + c8, y, res[p % kDepth], keep[p % kDepth]);
-        } else {
-          finish8<EPI>(ep, N, row, n0 + c8, y);
+          if (p + kDepth < kPasses) load_residual(p + kDepth, res[p % kDepth], keep[p % kDepth]);
         }
       }
-      if constexpr (kResidual) {
-        if (p + kDepth < kPasses) load_residual(p + kDepth, res[p % kDepth], keep[p % kDepth]);
-      }
+    };
+    // one verdict per wavefront (the flag only ever turns on)
+    if (EPI == kEpiBiasGelu && __builtin_amdgcn_readfirstlane(gelu_flag) != 0) {
+      passes(true);
+    } else {
+      passes(false);
     }
   } else {
     const int D = ep.d_model;
@@ -1057,13 +1088,14 @@ hipError_t launch_split(const bf16_t* A, const bf16_t* W, int M, int N, int K, i
   return hipGetLastError();
 }
 
-// Fills g_gelu_table on the current device before its first GELU product.
-// The fill runs on the caller's stream, which is then synchronised once, so
-// products on other streams find the table complete; inside a stream capture
-// the fill is recorded into the graph instead (stream order covers the
-// graph's products) and the device stays unmarked.
+// Enqueues the GELU table fill and its ready flag on the caller's stream
+// before the device's first GELU product (no host synchronisation; products
+// that run before the flag is set evaluate the erf).  Inside a stream capture
+// the two launches are recorded into the graph, whose replays then refill
+// the table, and the device stays unmarked so that a later uncaptured call
+// fills it outside the graph.
 std::mutex g_gelu_mutex;
-bool g_gelu_ready[64] = {false};
+bool g_gelu_enqueued[64] = {false};
 
 hipError_t ensure_gelu_table(hipStream_t st) {
   int dev = 0;
@@ -1071,15 +1103,14 @@ hipError_t ensure_gelu_table(hipStream_t st) {
   if (e != hipSuccess) return e;
   if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
   std::lock_guard<std::mutex> guard(g_gelu_mutex);
-  if (g_gelu_ready[dev]) return hipSuccess;
+  if (g_gelu_enqueued[dev]) return hipSuccess;
   hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
   e = hipStreamIsCapturing(st, &capture);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(gelu_table_kernel, dim3(256), dim3(256), 0, st);
+  hipLaunchKernelGGL(gelu_ready_kernel, dim3(1), dim3(1), 0, st);
   e = hipGetLastError();
-  if (e != hipSuccess || capture != hipStreamCaptureStatusNone) return e;
-  e = hipStreamSynchronize(st);
-  if (e == hipSuccess) g_gelu_ready[dev] = true;
+  if (e == hipSuccess && capture == hipStreamCaptureStatusNone) g_gelu_enqueued[dev] = true;
   return e;
 }
 
