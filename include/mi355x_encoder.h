@@ -6,7 +6,11 @@
  * Conventions shared by every entry point:
  *   - All tensors are raw device pointers owned by the caller.  The library
  *     never allocates or frees device memory and never synchronises the host,
- *     so every call is safe inside HIP graph capture.
+ *     so every call is safe inside HIP graph capture.  Its only device memory
+ *     is static, per GPU: the scratch array of the no-allocation forward and
+ *     a 128 KiB table of the GELU of every bf16 value, which the first GELU
+ *     product on a device fills with two launches on the caller's stream
+ *     (recorded into the graph when that first product is captured).
  *   - bf16 tensors are passed as `void*` to 16-bit storage (IEEE bfloat16).
  *     Activations are dense row-major; weights use nn.Linear's [out, in]
  *     row-major layout, exactly as they sit in a PyTorch state_dict.
