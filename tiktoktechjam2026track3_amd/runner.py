@@ -71,12 +71,14 @@ ENCODER_CONFIG_NAMES = tuple(sorted(ENCODER_CONFIGS))
 
 
 def resolve_device(device_arg: str) -> torch.device:
-    if device_arg == "auto":
-        return torch.device("cuda" if torch.cuda.is_available() else "cpu")
-    device = torch.device(device_arg)
-    if device.type == "cuda" and not torch.cuda.is_available():
-        raise RuntimeError("a GPU was requested, but torch.cuda.is_available() is False")
-    return device
+    """`--device`: "auto" takes the GPU when one is visible, else the CPU; an
+    explicit GPU device without a visible GPU is an error (reference
+    runner.py:48-54)."""
+    have_gpu = torch.cuda.is_available()
+    chosen = torch.device(("cuda" if have_gpu else "cpu") if device_arg == "auto" else device_arg)
+    if chosen.type == "cuda" and not have_gpu:
+        raise RuntimeError(f"--device {device_arg} needs a GPU, and torch.cuda.is_available() is False")
+    return chosen
 
 
 def resolve_dtype(dtype_name: str) -> torch.dtype:
@@ -84,17 +86,22 @@ def resolve_dtype(dtype_name: str) -> torch.dtype:
 
 
 def release_case_memory(device: torch.device) -> None:
+    """Between cases: collect the finished case's objects, and on a GPU return
+    the caching allocator's free blocks, so the next case starts from the
+    device's full memory (reference runner.py:66-69)."""
     gc.collect()
-    if device.type == "cuda":
-        torch.cuda.empty_cache()
+    if device.type != "cuda":
+        return
+    torch.cuda.empty_cache()
 
 
 def maybe_compile(model: nn.Module, enabled: bool, mode: str) -> nn.Module:
-    if not enabled:
-        return model
-    if not hasattr(torch, "compile"):
-        raise RuntimeError("this PyTorch build does not provide torch.compile")
-    return torch.compile(model, mode=mode)
+    """`--compile-baseline` / `--compile-user`: wrap the model in torch.compile
+    with the chosen mode (reference runner.py:72-77)."""
+    compile_fn = getattr(torch, "compile", None) if enabled else None
+    if enabled and compile_fn is None:
+        raise RuntimeError("--compile-* needs torch.compile, which this PyTorch build lacks")
+    return compile_fn(model, mode=mode) if enabled else model
 
 
 def parse_args(argv: Optional[Sequence[str]] = None) -> argparse.Namespace:
@@ -267,14 +274,14 @@ def settings_metadata(args: argparse.Namespace) -> Dict[str, object]:
 
 
 def json_safe(value: Any) -> Any:
-    """Non-finite numbers become strict JSON nulls."""
-    if isinstance(value, float) and not math.isfinite(value):
-        return None
+    """A copy of a result document that strict JSON accepts: NaN and +-inf
+    become null at any depth of dicts, lists and tuples (tuples become
+    lists, as json.dumps writes them anyway)."""
     if isinstance(value, dict):
-        return {key: json_safe(item) for key, item in value.items()}
+        return dict(zip(value.keys(), map(json_safe, value.values())))
     if isinstance(value, (list, tuple)):
-        return [json_safe(item) for item in value]
-    return value
+        return list(map(json_safe, value))
+    return None if isinstance(value, float) and (math.isnan(value) or math.isinf(value)) else value
 
 
 def write_json_document(path: Optional[Path], result: Dict[str, object]) -> None:
