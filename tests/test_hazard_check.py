@@ -76,3 +76,30 @@ def test_packed_fp32_instructions_are_listed():
     text += line(0x100C, "s_endpgm")
     report = hazard_check.check_text(text)
     assert len(report.packed_fp32) == 1 and "v_pk_fma_f32" in report.packed_fp32[0]
+
+
+def test_device_pass_ignoring_the_packed_fp32_flag_fails_the_build(monkeypatch, tmp_path):
+    """build_native compiles a probe kernel device-only with the build's flags
+    first: the host pass's unknown-feature note is expected, the same note
+    from the device pass means -packed-fp32-ops was ignored for gfx950 and
+    must stop the build.  (subprocess is replaced: no compiler runs.)"""
+    import subprocess
+
+    import pytest
+
+    from tiktoktechjam2026track3_amd import build_native
+
+    monkeypatch.setattr(build_native, "BUILD_DIR", tmp_path)
+
+    def fake_run(stdout_text):
+        def run(cmd, **kwargs):
+            assert "--cuda-device-only" in cmd
+            return subprocess.CompletedProcess(cmd, 0, stdout=stdout_text)
+        return run
+
+    monkeypatch.setattr(build_native.subprocess, "run", fake_run(""))
+    build_native._check_device_feature_flag("hipcc")  # silent device pass: fine
+    note = "'-packed-fp32-ops' is not a recognized feature for this target (ignoring feature)\n"
+    monkeypatch.setattr(build_native.subprocess, "run", fake_run(note))
+    with pytest.raises(RuntimeError, match="ignores -packed-fp32-ops"):
+        build_native._check_device_feature_flag("hipcc")

@@ -74,12 +74,38 @@ def _hipcc() -> str:
     return candidate
 
 
+# Text of the warning clang prints for a target feature it does not know.  The
+# host (x86) pass of every hipcc compile prints it for -packed-fp32-ops; the
+# device pass must not (_check_device_feature_flag), and the built code is
+# scanned for packed FP32 instructions as well (_check_mfma_hazards).
+_UNKNOWN_FEATURE = "is not a recognized feature for this target"
+
+
+def _check_device_feature_flag(hipcc: str) -> None:
+    """Fail when the gfx950 device pass does not recognise -packed-fp32-ops:
+    a device-only compile of a small kernel with the build's flags must be
+    free of the unknown-feature warning that the host pass prints."""
+    probe_dir = BUILD_DIR / "feature_probe"
+    probe_dir.mkdir(parents=True, exist_ok=True)
+    src = probe_dir / "probe.hip"
+    src.write_text(
+        "#include <hip/hip_runtime.h>\n"
+        "typedef float f2 __attribute__((ext_vector_type(2)));\n"
+        "__global__ void probe(f2* a, const f2* b) { a[threadIdx.x] = a[threadIdx.x] * b[threadIdx.x] + b[0]; }\n"
+    )
+    cmd = [hipcc, *COMMON_FLAGS, "--cuda-device-only", "-c", str(src), "-o", str(probe_dir / "probe.o")]
+    proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"device feature probe failed: {' '.join(cmd)}\n{proc.stdout}")
+    if _UNKNOWN_FEATURE in proc.stdout:
+        raise RuntimeError("the gfx950 device pass ignores -packed-fp32-ops:\n" + proc.stdout.strip())
+
+
 def _run(cmd: list[str]) -> None:
     proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
-    # hipcc's host pass does not know the device feature; whether the device
-    # pass applied it is checked on the built code (no packed FP32 instructions,
-    # _check_mfma_hazards)
-    noise = "is not a recognized feature for this target"
+    # the host pass's unknown-feature note (the device pass is checked by
+    # _check_device_feature_flag before any source is compiled)
+    noise = _UNKNOWN_FEATURE
     output = "\n".join(
         line for line in proc.stdout.splitlines() if noise not in line
     ).strip()
@@ -93,6 +119,7 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     """Compile every HIP source for gfx950 and link the shared library."""
     hipcc = _hipcc()
     BUILD_DIR.mkdir(parents=True, exist_ok=True)
+    _check_device_feature_flag(hipcc)
     include = f"-I{PACKAGE_DIR.parent / 'include'}"
     objects = []
     commands = []
