@@ -84,18 +84,66 @@ layernorm_kernel(const bf16_t* __restrict__ x, const bf16_t* __restrict__ gamma,
       for (int e = 0; e < 4; ++e) st[w] = welford_add(st[w], v[s][e]);
     }
   }
-  // shuffle-down trees of the four virtual warps (lane 0 holds each result)
+  float mean_all, m2_all;
+  if constexpr (WIDTH >= 1024) {
+    // Every virtual thread holds the same number of elements, so the four
+    // trees can share registers once half of a tree's lanes are idle: each
+    // merge below pairs the same two virtual lanes, in the same operand
+    // order, as the per-warp tree.
+    // Level 32 per virtual warp: lanes 0..31 of each hold its live states.
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
+    for (int w = 0; w < 4; ++w) st[w] = welford_merge(st[w], shfl_down(st[w], 32));
+    // Pack: p01 = warp 0 in lanes 0..31, warp 1 in lanes 32..63; p23 likewise.
+    const bool upper32 = lane >= 32;
+    Welford p01 = st[0], p23 = st[2];
+    {
+      const float m1 = __shfl_xor(st[1].mean, 32, kWave), q1 = __shfl_xor(st[1].m2, 32, kWave);
+      const float m3 = __shfl_xor(st[3].mean, 32, kWave), q3 = __shfl_xor(st[3].m2, 32, kWave);
+      if (upper32) {
+        p01.mean = m1;
+        p01.m2 = q1;
+        p23.mean = m3;
+        p23.m2 = q3;
+      }
+    }
+    // Level 16 within each 32-lane half.
+    p01 = welford_merge(p01, shfl_down(p01, 16));
+    p23 = welford_merge(p23, shfl_down(p23, 16));
+    // Pack: q = warp 0 | warp 2 | warp 1 | warp 3 in lanes 0..15 | 16..31 |
+    // 32..47 | 48..63 (lanes with bit 4 set take p23 from lane ^ 16).
+    Welford q = p01;
+    {
+      const float m = __shfl_xor(p23.mean, 16, kWave), q2 = __shfl_xor(p23.m2, 16, kWave);
+      if (lane & 16) {
+        q.mean = m;
+        q.m2 = q2;
+      }
+    }
+    // Levels 8..1 within each 16-lane group: lanes 0, 16, 32, 48 end with the
+    // totals of warps 0, 2, 1, 3.
 #pragma unroll
-    for (int w = 0; w < 4; ++w) st[w] = welford_merge(st[w], shfl_down(st[w], off));
+    for (int off = 8; off > 0; off >>= 1) q = welford_merge(q, shfl_down(q, off));
+    // Cross-warp merges: (0 <- 2) at lane 0, (1 <- 3) at lane 32, then (0 <- 1).
+    q = welford_merge(q, shfl_down(q, 16));
+    q = welford_merge(q, shfl_down(q, 32));
+    mean_all = q.mean;
+    m2_all = q.m2;
+  } else {
+    // shuffle-down trees of the four virtual warps (lane 0 holds each result)
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) st[w] = welford_merge(st[w], shfl_down(st[w], off));
+    }
+    // cross-warp merges: (0 <- 2), (1 <- 3), then (0 <- 1)
+    Welford w0 = welford_merge(st[0], st[2]);
+    const Welford w1 = welford_merge(st[1], st[3]);
+    w0 = welford_merge(w0, w1);
+    mean_all = w0.mean;
+    m2_all = w0.m2;
   }
-  // cross-warp merges: (0 <- 2), (1 <- 3), then (0 <- 1)
-  Welford w0 = welford_merge(st[0], st[2]);
-  const Welford w1 = welford_merge(st[1], st[3]);
-  w0 = welford_merge(w0, w1);
-  const float mean = __shfl(w0.mean, 0, kWave);
-  const float var = __shfl(w0.m2, 0, kWave) / static_cast<float>(WIDTH);
+  const float mean = __shfl(mean_all, 0, kWave);
+  const float var = __shfl(m2_all, 0, kWave) / static_cast<float>(WIDTH);
   const float rstd = rsqrtf(var + eps);
 
   if (!has) return;
