@@ -420,27 +420,34 @@ struct BigTile {
   __device__ static constexpr int swz(int row) { return kChunks == 8 ? (row & 7) : ((row >> 1) & 3); }
 };
 
-// r / keep: the residual's 8 values and the row-mask verdict, loaded ahead
-// by the caller (residual epilogues only).
+// v: 8 consecutive outputs y = bf16(acc + bias) of one row, two per word
+// (low half first).  r / keep: the residual's 8 values and the row-mask
+// verdict, loaded ahead by the caller (residual epilogues only).
 template <int EPI>
-__device__ __forceinline__ void finish8(const GemmEpilogueArgs& ep, int N, int row, int col,
-                                        const float (&y)[8], u32x4 r = u32x4{0u, 0u, 0u, 0u},
-                                        bool keep = true, bool gelu_table = false) {
+__device__ __forceinline__ void finish8(const GemmEpilogueArgs& ep, int N, int row, int col, u32x4 v,
+                                        u32x4 r = u32x4{0u, 0u, 0u, 0u}, bool keep = true,
+                                        bool gelu_table = false) {
   const int64_t idx = static_cast<int64_t>(row) * N + col;
   u32x4 w;
   if constexpr (EPI == kEpiBias) {
-    w = u32x4{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]), pack_bf16x2(y[4], y[5]), pack_bf16x2(y[6], y[7])};
+    w = v;
   } else if constexpr (EPI == kEpiBiasGelu) {
     if (gelu_table) {
-      // y holds bf16 values: the table lookup is the erf GELU of each
+      // the table entry of a bf16 pattern is the erf GELU of that value
       uint32_t g[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) g[e] = g_gelu_table[__float_as_uint(y[e]) >> 16];
+      for (int e = 0; e < 4; ++e) {
+        g[2 * e] = g_gelu_table[v[e] & 0xffffu];
+        g[2 * e + 1] = g_gelu_table[v[e] >> 16];
+      }
       w = u32x4{g[0] | (g[1] << 16), g[2] | (g[3] << 16), g[4] | (g[5] << 16), g[6] | (g[7] << 16)};
     } else {
       float g[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) g[e] = gelu_erf(y[e]);
+      for (int e = 0; e < 4; ++e) {
+        g[2 * e] = gelu_erf(lo_bf16(v[e]));
+        g[2 * e + 1] = gelu_erf(hi_bf16(v[e]));
+      }
       w = u32x4{pack_bf16x2(g[0], g[1]), pack_bf16x2(g[2], g[3]), pack_bf16x2(g[4], g[5]), pack_bf16x2(g[6], g[7])};
     }
   } else {
@@ -448,8 +455,8 @@ __device__ __forceinline__ void finish8(const GemmEpilogueArgs& ep, int N, int r
       float o[8];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        o[2 * e] = lo_bf16(r[e]) + y[2 * e];
-        o[2 * e + 1] = hi_bf16(r[e]) + y[2 * e + 1];
+        o[2 * e] = lo_bf16(r[e]) + lo_bf16(v[e]);
+        o[2 * e + 1] = hi_bf16(r[e]) + hi_bf16(v[e]);
       }
       w = u32x4{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]), pack_bf16x2(o[4], o[5]), pack_bf16x2(o[6], o[7])};
     } else {
@@ -716,23 +723,25 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
     for (int p = 0; p < kDepth; ++p) load_residual(p, res[p], keep[p]);
   }
   __syncthreads();
+  // Every row of the tile is in range (all tiles but the last tile row): the
+  // passes then run without a per-row branch, so the compiler can batch their
+  // LDS reads and stores.  Uniform.
+  const bool full = m0 + BM <= M;
 
   if constexpr (EPI != kEpiQkvHeadMajor) {
-    // one verdict per wavefront (the flag only ever turns on)
-    // the passes, with the GELU's table (or erf) fixed for the whole loop
-    auto passes = [&](bool gelu_table) __attribute__((always_inline)) {
+    // the passes, with the GELU's table (or erf) and the range check fixed
+    // for the whole loop
+    auto passes = [&](bool gelu_table, bool all_rows) __attribute__((always_inline)) {
 #pragma unroll
       for (int p = 0; p < kPasses; ++p) {
         const int rl = rl0 + p * kRowsPerPass;
         const int row = m0 + rl;
-        if (row < M) {
+        if (all_rows || row < M) {
           const u32x4 v = *reinterpret_cast<const u32x4*>(sc + rl * T::kLdc + c8);
-          const float y[8] = {lo_bf16(v[0]), hi_bf16(v[0]), lo_bf16(v[1]), hi_bf16(v[1]),
-                              lo_bf16(v[2]), hi_bf16(v[2]), lo_bf16(v[3]), hi_bf16(v[3])};
           if constexpr (kResidual) {
-            finish8<EPI>(ep, N, row, n0 + c8, y, res[p % kDepth], keep[p % kDepth]);
+            finish8<EPI>(ep, N, row, n0 + c8, v, res[p % kDepth], keep[p % kDepth]);
           } else {
-            finish8<EPI>(ep, N, row, n0 + c8, y, u32x4{0u, 0u, 0u, 0u}, true, gelu_table);
+            finish8<EPI>(ep, N, row, n0 + c8, v, u32x4{0u, 0u, 0u, 0u}, true, gelu_table);
           }
         }
         if constexpr (kResidual) {
@@ -740,58 +749,118 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
         }
       }
     };
-    // one verdict per wavefront (the flag only ever turns on)
-    if (EPI == kEpiBiasGelu && __builtin_amdgcn_readfirstlane(gelu_flag) != 0) {
-      passes(true);
+    // One verdict per wavefront (the flag only ever turns on).  The GELU
+    // keeps the per-row branch on full tiles too: batched without it, the
+    // table's gathers ran 1-3% slower (32768x4096x1024, 409600x1024x1024).
+    const bool table = EPI == kEpiBiasGelu && __builtin_amdgcn_readfirstlane(gelu_flag) != 0;
+    if (table) {
+      passes(true, false);
+    } else if (EPI != kEpiBiasGelu && full) {
+      passes(false, true);
     } else {
-      passes(false);
+      passes(false, false);
     }
   } else {
     const int D = ep.d_model;
     const int hd = ep.head_dim;
     const int S = ep.seq_len;
-    // Q / K: 8 consecutive channels of one head, one row
+    // Row m0 + rl of the tile is sequence position s of batch b.  On a full
+    // tile whose row stride is at most S both loops below carry s and the
+    // element offset along (one wrap into the next sequence per step at
+    // most); otherwise each row divides.
+    auto locate = [&](int row, int& b, int& s) {
+      b = row / S;
+      s = row - b * S;
+    };
+    // Q / K: 8 consecutive channels of one head, one row; the thread's
+    // channels are the same in every pass.  Element offset of (b, s):
+    // ((b H + h) S + s) hd + d.
     const int col = n0 + c8;
     const int which = col / D;
     if (which < 2) {
       const int h = (col - which * D) / hd;
       const int d = (col - which * D) - h * hd;
       bf16_t* dst = which == 0 ? ep.q : ep.k;
-      for (int rl = tid / kPerRow; rl < BM; rl += kThreads / kPerRow) {
-        const int row = m0 + rl;
-        if (row >= M) break;
-        const int b = row / S;
-        const int s = row - b * S;
-        *reinterpret_cast<u32x4*>(dst + ((static_cast<int64_t>(b) * ep.num_heads + h) * S + s) * hd + d) =
-            *reinterpret_cast<const u32x4*>(sc + rl * T::kLdc + c8);
+      auto offset = [&](int b, int s) {
+        return ((static_cast<int64_t>(b) * ep.num_heads + h) * S + s) * hd + d;
+      };
+      if (full && kRowsPerPass <= S) {
+        int b, s;
+        locate(m0 + rl0, b, s);
+        int64_t off = offset(b, s);
+        const int64_t wrap_off = (static_cast<int64_t>(ep.num_heads) - 1) * S * hd;  // next batch, s - S
+#pragma unroll
+        for (int p = 0; p < kPasses; ++p) {
+          *reinterpret_cast<u32x4*>(dst + off) =
+              *reinterpret_cast<const u32x4*>(sc + (rl0 + p * kRowsPerPass) * T::kLdc + c8);
+          s += kRowsPerPass;
+          off += kRowsPerPass * hd;
+          const bool wrap = s >= S;
+          s = wrap ? s - S : s;
+          off = wrap ? off + wrap_off : off;
+        }
+      } else {
+        for (int rl = rl0; rl < BM; rl += kRowsPerPass) {
+          const int row = m0 + rl;
+          if (row >= M) break;
+          int b, s;
+          locate(row, b, s);
+          *reinterpret_cast<u32x4*>(dst + offset(b, s)) = *reinterpret_cast<const u32x4*>(sc + rl * T::kLdc + c8);
+        }
       }
     }
-    // V^T: one channel, 8 consecutive rows (sequence positions)
-    for (int item = tid; item < BN * (BM / 8); item += kThreads) {
-      const int cl = item % BN;
-      const int r8 = (item / BN) * 8;
-      const int vcol = n0 + cl;
-      if (vcol / D != 2) continue;
+    // V^T: one channel, 8 consecutive rows (sequence positions).  Thread t
+    // owns channel t % BN of the tile and row groups t / BN, t / BN + kVStep,
+    // ... of 8 rows each.  Element offset of (b, s): b H hd ld + (h hd + d) ld + s.
+    static_assert(kThreads % BN == 0, "one channel per thread");
+    constexpr int kVStep = kThreads / BN;
+    const int cl = tid % BN;
+    const int vcol = n0 + cl;
+    if (vcol / D == 2) {
       const int h = (vcol - 2 * D) / hd;
       const int d = (vcol - 2 * D) - h * hd;
-      const int row0 = m0 + r8;
-      if (row0 >= M) continue;
-      const int b0 = row0 / S;
-      const int s0 = row0 - b0 * S;
-      bf16_t* dst = ep.v_t + ((static_cast<int64_t>(b0) * ep.num_heads + h) * hd + d) * ep.ld_vt + s0;
-      if (row0 + 7 < M && s0 + 7 < S && (s0 & 7) == 0 && (ep.ld_vt & 7) == 0) {
-        uint32_t p[4];
+      bf16_t* vrow = ep.v_t + (static_cast<int64_t>(h) * hd + d) * ep.ld_vt;
+      const int64_t batch_stride = static_cast<int64_t>(ep.num_heads) * hd * ep.ld_vt;
+      // 8-row groups that never straddle a sequence and land 16-byte aligned
+      if (full && (S & 7) == 0 && (ep.ld_vt & 7) == 0 && 8 * kVStep <= S) {
+        int b, s;
+        locate(m0 + (tid / BN) * 8, b, s);
+        int64_t off = b * batch_stride + s;
+        for (int g = tid / BN; g < BM / 8; g += kVStep) {
+          const int r8 = g * 8;
+          uint32_t p[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          p[e] = static_cast<uint32_t>(sc[(r8 + 2 * e) * T::kLdc + cl]) |
-                 (static_cast<uint32_t>(sc[(r8 + 2 * e + 1) * T::kLdc + cl]) << 16);
-        *reinterpret_cast<u32x4*>(dst) = u32x4{p[0], p[1], p[2], p[3]};
+          for (int e = 0; e < 4; ++e)
+            p[e] = static_cast<uint32_t>(sc[(r8 + 2 * e) * T::kLdc + cl]) |
+                   (static_cast<uint32_t>(sc[(r8 + 2 * e + 1) * T::kLdc + cl]) << 16);
+          *reinterpret_cast<u32x4*>(vrow + off) = u32x4{p[0], p[1], p[2], p[3]};
+          s += 8 * kVStep;
+          off += 8 * kVStep;
+          const bool wrap = s >= S;
+          s = wrap ? s - S : s;
+          off = wrap ? off + batch_stride - S : off;
+        }
       } else {
-        for (int e = 0; e < 8 && row0 + e < M; ++e) {
-          const int row = row0 + e;
-          const int b = row / S;
-          const int s = row - b * S;
-          ep.v_t[((static_cast<int64_t>(b) * ep.num_heads + h) * hd + d) * ep.ld_vt + s] = sc[(r8 + e) * T::kLdc + cl];
+        for (int g = tid / BN; g < BM / 8; g += kVStep) {
+          const int r8 = g * 8;
+          const int row0 = m0 + r8;
+          if (row0 >= M) break;
+          int b0, s0;
+          locate(row0, b0, s0);
+          if (row0 + 7 < M && s0 + 7 < S && (s0 & 7) == 0 && (ep.ld_vt & 7) == 0) {
+            uint32_t p[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              p[e] = static_cast<uint32_t>(sc[(r8 + 2 * e) * T::kLdc + cl]) |
+                     (static_cast<uint32_t>(sc[(r8 + 2 * e + 1) * T::kLdc + cl]) << 16);
+            *reinterpret_cast<u32x4*>(vrow + b0 * batch_stride + s0) = u32x4{p[0], p[1], p[2], p[3]};
+          } else {
+            for (int e = 0; e < 8 && row0 + e < M; ++e) {
+              int b, s;
+              locate(row0 + e, b, s);
+              vrow[b * batch_stride + s] = sc[(r8 + e) * T::kLdc + cl];
+            }
+          }
         }
       }
     }
