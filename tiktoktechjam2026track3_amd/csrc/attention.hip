@@ -49,9 +49,11 @@ hipError_t expf_selfcheck(uint32_t lo_bits, uint32_t hi_bits, uint32_t* mismatch
   return hipGetLastError();
 }
 
-bool attention_seq_supported(int64_t seq_len) {
+bool attention_seq_supported(int64_t seq_len, int64_t head_dim) {
   // torch's long-row softmax folds 4-element vectors; other lengths are not pinned
-  return seq_len <= kWarpSoftmaxMaxKeys || seq_len % 4 == 0;
+  if (!(seq_len <= kWarpSoftmaxMaxKeys || seq_len % 4 == 0)) return false;
+  // the tile loads address one head's K and V^T with 32-bit byte offsets
+  return vt_stride(seq_len) * head_dim * 2 < (int64_t(1) << 32);
 }
 
 hipError_t attention_fwd_bf16(const bf16_t* q, const bf16_t* k, const bf16_t* v_t, bf16_t* ctx,

@@ -4,8 +4,8 @@
 //
 // Scores are never materialised: each workgroup owns BQ = NW * 32 query rows
 // of one (batch, head) (32 per wavefront) and streams 64-key tiles of K (and
-// V^T) through a two-stage LDS ring filled with direct global->LDS loads
-// (global_load_lds_dwordx4).  Both products put the query on the MFMA N
+// V^T) through a two-stage LDS ring filled with direct buffer->LDS loads
+// (buffer_load_dwordx4 ... lds).  Both products put the query on the MFMA N
 // dimension (the lane), so every per-query quantity lives in the lane that owns
 // the query (lane l: query l%32, key half l/32):
 //   S^T[key, q]  = K[key, :] . Q[q, :]        A = K tile (LDS), B = Q (registers)
@@ -55,6 +55,8 @@
 // in the reference, and adding 0 leaves a partial sum unchanged, so skipping
 // them is exact.
 #pragma once
+
+#include <type_traits>
 
 #include "common.h"
 #include "kernels.h"
@@ -242,21 +244,36 @@ attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
   // (64 / (HD / 8)) slab .. +, lane L writing row first + L / (HD / 8), slot
   // L % (HD / 8); V^T rows 8 slab .. +7, lane L writing row 8 slab + L / 8,
   // slot L % 8.  Each lane fetches the chunk that its slot holds.
+  // The loads are buffer loads on one resource per head for K and one for
+  // V^T: a lane's byte offset inside its slab is fixed for the whole kernel
+  // (computed here once), and the tile's position is a uniform soffset, so a
+  // load costs no per-tile address arithmetic.  The host keeps one head's K
+  // and V^T under 4 GiB (attention_seq_supported).
+  constexpr int kLoadsPerWave = (kSlabs + NW - 1) / NW;
+  const i32x4 k_rsrc = buffer_rsrc(Kh);
+  const i32x4 v_rsrc = buffer_rsrc(Vh);
+  int k_voff[kLoadsPerWave], v_voff[kLoadsPerWave];
+#pragma unroll
+  for (int j = 0; j < kLoadsPerWave; ++j) {
+    const int slab = NW * j + wave;  // past kSlabs only when unused below
+    const int rk = (kWave / kChunksK) * slab + lane / kChunksK;
+    k_voff[j] = (rk * HD + ((lane % kChunksK) ^ k_swz<HD>(rk)) * 8) * 2;
+    const int rv = 8 * slab + (lane >> 3);
+    // (unsigned: a head's V^T may exceed 2 GiB)
+    v_voff[j] = static_cast<int>((static_cast<uint32_t>(rv) * static_cast<uint32_t>(ld_vt) +
+                                  static_cast<uint32_t>(((lane & 7) ^ v_swz(rv)) * 8)) * 2u);
+  }
   auto issue_full = [&](int buf, int k0, bool with_v) {
 #pragma unroll
-    for (int j = 0; j < (kSlabs + NW - 1) / NW; ++j) {
+    for (int j = 0; j < kLoadsPerWave; ++j) {
       const int slab = NW * j + wave;
       if (kSlabs % NW != 0 && slab >= kSlabs) break;  // uniform per wavefront
       const int rk0 = (kWave / kChunksK) * slab;
-      const int rk = rk0 + lane / kChunksK;
-      const int ck = (lane % kChunksK) ^ k_swz<HD>(rk);
-      __builtin_amdgcn_global_load_lds(Kh + static_cast<int64_t>(k0 + rk) * HD + ck * 8,
-                                       &sK[buf * kTileElems + rk0 * HD], 16, 0, 0);
+      enc_buffer_load_lds(k_rsrc, lds_ptr(&sK[buf * kTileElems + rk0 * HD]), 16, k_voff[j],
+                          static_cast<int>(static_cast<uint32_t>(k0) * (HD * 2u)), 0, 0);
       if (with_v) {
         const int rv0 = 8 * slab;
-        const int cv = (lane & 7) ^ v_swz(rv0 + (lane >> 3));
-        __builtin_amdgcn_global_load_lds(Vh + static_cast<int64_t>(rv0 + (lane >> 3)) * ld_vt + k0 + cv * 8,
-                                         &sV[buf * kTileElems + rv0 * kBKV], 16, 0, 0);
+        enc_buffer_load_lds(v_rsrc, lds_ptr(&sV[buf * kTileElems + rv0 * kBKV]), 16, v_voff[j], k0 * 2, 0, 0);
       }
     }
   };
@@ -318,14 +335,31 @@ attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
       __builtin_amdgcn_s_waitcnt(kWaitVm0);
       __syncthreads();
       int it = 0;
-      for (; it < active; ++it) {
-        const int cur = it & 1;
+      // Iteration `it` reads buffer it & 1.  For long rows the loop runs two
+      // iterations per trip with the buffer index a constant in each, so the
+      // bodies' LDS addresses fold into instruction offsets instead of being
+      // recomputed per tile (c5 4%, c4 6% faster).  The warp-order bodies
+      // (device expf) are twice as long: unrolled, the c3 kernel grew to
+      // 64 KiB of code and ran 34% slower, so they keep one tile per trip.
+      auto step = [&](auto cur_c) {
+        constexpr int kCur = decltype(cur_c)::value;
+        const int cur = kCur >= 0 ? kCur : (it & 1);
         const int nt = next(tile);
         if (it + 1 < nkb) issue_tile(cur ^ 1, nt, with_v);
         body(cur, tile);
         __builtin_amdgcn_s_waitcnt(kWaitVm0);
         __syncthreads();
         tile = nt;
+        ++it;
+      };
+      if constexpr (BLOCK_ORDER) {
+        while (it + 1 < active) {
+          step(std::integral_constant<int, 0>{});
+          step(std::integral_constant<int, 1>{});
+        }
+        if (it < active) step(std::integral_constant<int, 0>{});  // it is even here
+      } else {
+        while (it < active) step(std::integral_constant<int, -1>{});
       }
       for (; it < nkb; ++it) {
         const int nt = next(tile);

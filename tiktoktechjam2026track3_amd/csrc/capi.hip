@@ -125,9 +125,9 @@ int check_encoder_shape(int64_t B, int64_t S, int64_t D, int64_t H, int64_t F, b
   if (!enc::layernorm_supported(D))
     return fail(ENC_ERR_UNSUPPORTED, "LayerNorm width must be a power of two in [32, 4096] (got " +
                                          std::to_string(D) + ")");
-  if (exact_attention && !enc::attention_seq_supported(S))
-    return fail(ENC_ERR_UNSUPPORTED, "seq_len above 2048 must be a multiple of 4 (got " +
-                                         std::to_string(S) + ")");
+  if (exact_attention && !enc::attention_seq_supported(S, hd))
+    return fail(ENC_ERR_UNSUPPORTED, "seq_len above 2048 must be a multiple of 4, and one head's keys under "
+                                     "4 GiB (got " + std::to_string(S) + ")");
   if (D % 32 != 0 || F % 32 != 0)
     return fail(ENC_ERR_UNSUPPORTED, "d_model and ffn_dim must be multiples of 32");
   if (B * S >= (int64_t(1) << 31)) return fail(ENC_ERR_UNSUPPORTED, "batch * seq_len must be < 2^31");
@@ -503,8 +503,9 @@ int attention_entry(bool exact, const void* q, const void* k, const void* v_t, v
                                            : "online attention: head_dim must be 64");
   if (kv_len && key_mask) return fail(ENC_ERR_INVALID, "attention: pass kv_len or key_mask, not both");
   if (!(scale > 0.f)) return fail(ENC_ERR_INVALID, "attention: scale must be positive");
-  if (exact && !enc::attention_seq_supported(seq_len))
-    return fail(ENC_ERR_UNSUPPORTED, "attention: seq_len above 2048 must be a multiple of 4");
+  if (exact && !enc::attention_seq_supported(seq_len, head_dim))
+    return fail(ENC_ERR_UNSUPPORTED,
+                "attention: seq_len above 2048 must be a multiple of 4, and one head's keys under 4 GiB");
   if (seq_len >= (int64_t(1) << 30) || batch * num_heads * ((seq_len + 31) / 32) >= (int64_t(1) << 31))
     return fail(ENC_ERR_UNSUPPORTED, "attention: grid too large");
   auto fn = exact ? enc::attention_fwd_bf16 : enc::flash_attention_fwd_bf16;

@@ -4,6 +4,14 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+// Raw buffer load into LDS (the LLVM intrinsic, bound by name): byte address =
+// resource base + soffset + voffset; the LDS destination is the instruction's
+// uniform base (M0) plus `size` bytes per lane.
+typedef int32_t enc_rsrc_t __attribute__((ext_vector_type(4)));
+__device__ void enc_buffer_load_lds(enc_rsrc_t rsrc, __attribute__((address_space(3))) uint32_t* lds, int size,
+                                    int voffset, int soffset, int offset, int aux)
+    __asm("llvm.amdgcn.raw.buffer.load.lds");
+
 namespace enc {
 
 typedef uint16_t bf16_t;  // IEEE bfloat16 storage
@@ -101,6 +109,21 @@ constexpr int waitcnt_imm(int vm, int lgkm) {
 // it needs finished; the memory clobber keeps the compiler from moving LDS
 // accesses across the barrier.
 __device__ __forceinline__ void ring_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+// Buffer resource over [p, p + 4 GiB): stride 0, no range limit, the gfx9
+// raw-buffer format word.  Callers keep every load inside their own rows.
+__device__ __forceinline__ i32x4 buffer_rsrc(const void* p) {
+  const uint64_t a = reinterpret_cast<uint64_t>(p);
+  return i32x4{static_cast<int32_t>(static_cast<uint32_t>(a)),
+               static_cast<int32_t>(static_cast<uint32_t>(a >> 32) & 0xffffu), -1, 0x00020000};
+}
+
+// LDS address of a pointer into a __shared__ array, as the buffer-to-LDS load
+// takes it (the low 32 bits of the flat address are the LDS offset).
+__device__ __forceinline__ __attribute__((address_space(3))) uint32_t* lds_ptr(const void* p) {
+  return reinterpret_cast<__attribute__((address_space(3))) uint32_t*>(reinterpret_cast<uintptr_t>(p));
+}
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

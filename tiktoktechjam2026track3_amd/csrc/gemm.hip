@@ -28,14 +28,6 @@
 #include "kernels.h"
 #include "streamk_tail.h"
 
-// Raw buffer load into LDS (the LLVM intrinsic, bound by name): byte address =
-// resource base + soffset + voffset; the LDS destination is the instruction's
-// uniform base (M0) plus 16 bytes per lane.
-typedef int32_t enc_rsrc_t __attribute__((ext_vector_type(4)));
-__device__ void enc_buffer_load_lds(enc_rsrc_t rsrc, __attribute__((address_space(3))) uint32_t* lds, int size,
-                                    int voffset, int soffset, int offset, int aux)
-    __asm("llvm.amdgcn.raw.buffer.load.lds");
-
 namespace enc {
 
 namespace {
@@ -391,15 +383,6 @@ __device__ __forceinline__ void interleave() {
     for (int l = q * kLoadsPer; l < (q + 1) * kLoadsPer && l < LOADS; ++l)
       __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // global load
   }
-}
-
-typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
-// Buffer resource over [p, p + 4 GiB): stride 0, no range limit, the gfx9
-// raw-buffer format word.  The loads below stay inside their tile's rows.
-__device__ __forceinline__ i32x4 buffer_rsrc(const void* p) {
-  const uint64_t a = reinterpret_cast<uint64_t>(p);
-  return i32x4{static_cast<int32_t>(static_cast<uint32_t>(a)),
-               static_cast<int32_t>(static_cast<uint32_t>(a >> 32) & 0xffffu), -1, 0x00020000};
 }
 
 template <int BM, int BN, int BK, int NS>

@@ -121,8 +121,9 @@ bool block_tail_supported(int64_t d_model, int64_t ffn_dim);
 hipError_t block_tail_bf16(const BlockTailArgs& args, int64_t rows, int64_t d_model, int64_t ffn_dim, float eps,
                            int num_cus, hipStream_t stream);
 
-// Sequence lengths whose softmax summation order is reproduced exactly.
-bool attention_seq_supported(int64_t seq_len);
+// Sequence lengths whose softmax summation order is reproduced exactly, and
+// whose per-head K and V^T the exact kernel's 32-bit tile offsets reach.
+bool attention_seq_supported(int64_t seq_len, int64_t head_dim);
 
 // Counts (atomically, into *mismatches) the float bit patterns in
 // [lo_bits, hi_bits] where the attention's expf_nonpos differs from expf.
