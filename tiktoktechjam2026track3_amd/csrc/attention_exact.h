@@ -631,40 +631,44 @@ attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
     // n = r + 32 m holds the vectors of threads 16 r .. 16 r + 15.  Tiles are
     // visited residue-major; "warp" w covers residues 4w .. 4w+3.  All partial
     // arrays are indexed statically: the running residue's partials live in
-    // acc[], a finished residue is shifted into hist[] (oldest first), and a
-    // finished warp's sum is shifted into warp_sum[].
+    // acc[]; of a warp's finished residues r0..r3, r0 goes to h0 and r1 to h1,
+    // r2 is added to h0 as it finishes (r0 + r2, the tree's first pair), and
+    // r3 completes the warp: (r0 + r2) + (r1 + r3).  A finished warp's sum is
+    // shifted into warp_sum[].
     // successor in residue-major order: tiles r, r + 32, r + 64, ..., then r + 1
     auto resmajor = [&](int t) { return t + 32 < nkb ? t + 32 : (t & 31) + 1; };
     float warp_sum[8];
-    float hist[4][8];  // the current warp's finished residues, in order
-    float acc[8];      // [vector slot 4*kb32 + i] of the running residue
+    float h0[8], h1[8];  // the current warp's finished residues (see above)
+    float acc[8];        // [vector slot 4*kb32 + i] of the running residue
 #pragma unroll
     for (int w = 0; w < 8; ++w) warp_sum[w] = 0.f;
 #pragma unroll
     for (int v = 0; v < 8; ++v) {
       acc[v] = 0.f;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) hist[q][v] = 0.f;
+      h0[v] = 0.f;
+      h1[v] = 0.f;
     }
     int cur_res = 0;
-    // residue cur_res is complete: shift it into hist; after a warp's fourth
-    // residue, reduce the warp with a shuffle-down tree over
-    // lam = 16 rr + u, u = 8 kb32 + 4 (i>>1) + 2 h + (i&1):
+    // residue cur_res is complete: file it (uniform branch on its position in
+    // the warp); after a warp's fourth residue, reduce the warp with a
+    // shuffle-down tree over lam = 16 rr + u, u = 8 kb32 + 4 (i>>1) + 2 h + (i&1):
     // offsets 32, 16 (rr), 8 (kb32), 4 (i>>1), 2 (lane half), 1 (i&1)
     auto finish_residue = [&]() {
-#pragma unroll
-      for (int v = 0; v < 8; ++v) {
-        hist[0][v] = hist[1][v];
-        hist[1][v] = hist[2][v];
-        hist[2][v] = hist[3][v];
-        hist[3][v] = acc[v];
-        acc[v] = 0.f;
-      }
+      const int q = cur_res & 3;
       ++cur_res;
-      if ((cur_res & 3) == 0) {
+      if (q == 0) {
+#pragma unroll
+        for (int v = 0; v < 8; ++v) h0[v] = acc[v];
+      } else if (q == 1) {
+#pragma unroll
+        for (int v = 0; v < 8; ++v) h1[v] = acc[v];
+      } else if (q == 2) {
+#pragma unroll
+        for (int v = 0; v < 8; ++v) h0[v] = h0[v] + acc[v];
+      } else {
         float t8[8];
 #pragma unroll
-        for (int v = 0; v < 8; ++v) t8[v] = (hist[0][v] + hist[2][v]) + (hist[1][v] + hist[3][v]);
+        for (int v = 0; v < 8; ++v) t8[v] = h0[v] + (h1[v] + acc[v]);
         float t4[4];
 #pragma unroll
         for (int v = 0; v < 4; ++v) t4[v] = t8[v] + t8[v + 4];                   // offset 8 (kb32)
@@ -678,6 +682,8 @@ attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
         for (int w = 0; w < 7; ++w) warp_sum[w] = warp_sum[w + 1];
         warp_sum[7] = ws;
       }
+#pragma unroll
+      for (int v = 0; v < 8; ++v) acc[v] = 0.f;
     };
     sweep(resmajor, false, nkb, [&](int buf, int kb) {
       const int k0 = kb * kBKV;
