@@ -132,6 +132,9 @@ attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
   static_assert(HD == 8 || HD == 32 || HD == 64 || HD == 128 || HD == 256, "head_dim 8, 32, 64, 128 or 256");
   constexpr bool kSplit = NW == 2 && RES == 2;
   static_assert(NW != 2 || (RES == 2 && !BLOCK_ORDER), "two wavefronts: key split of two resident tiles");
+  // short-row regime with a power-of-two scale: gaps stay unscaled, the scale
+  // folds into expf's constants (exp_gap below)
+  constexpr bool kFoldScale = POW2_SCALE && !BLOCK_ORDER;
   constexpr int kThreads = NW * kWave;
   constexpr int kBQ = kSplit ? 32 : NW * 32;
   constexpr int kTileElems = kBKV * HD;  // one K or V^T tile, bf16 elements
@@ -541,17 +544,26 @@ attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
   // division verdict's exception (slow_div) every allowed key's gap is at
   // least kMinFastGap, and a tile with no excluded key holds no -inf, so the
   // underflow clamp (below -103.28) cannot fire there and is left out.
+  // exp(s - max) of a gap in the short-row regime.  With a power-of-two
+  // scale the gaps stay unscaled (g = bf16(q.k) - bf16(max raw dot)) and the
+  // scale is folded into expf's constants: the same bits as expf(g * scale),
+  // one multiply fewer per score.
+  const ExpfScaled ec = expf_scaled_consts(scale);
+  auto exp_gap = [&](float g) { return kFoldScale ? expf_nonpos_scaled(g, ec) : expf_nonpos(g); };
+  auto exp_gap_unclamped = [&](float g) {
+    return kFoldScale ? expf_nonpos_scaled_unclamped(g, ec) : expf_nonpos_unclamped(g);
+  };
   auto tile_exp = [&](f32x16 (&s)[2], bool clamp) {
     if (clamp) {
 #pragma unroll
       for (int kb32 = 0; kb32 < 2; ++kb32)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) s[kb32][r] = expf_nonpos(s[kb32][r]);
+        for (int r = 0; r < 16; ++r) s[kb32][r] = exp_gap(s[kb32][r]);
     } else {
 #pragma unroll
       for (int kb32 = 0; kb32 < 2; ++kb32)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) s[kb32][r] = expf_nonpos_unclamped(s[kb32][r]);
+        for (int r = 0; r < 16; ++r) s[kb32][r] = exp_gap_unclamped(s[kb32][r]);
     }
   };
 
@@ -568,7 +580,7 @@ attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
     if constexpr (kSplit) {
       // this wavefront's weights, zeros for a tile no query of the block sees
       if (wave < active) {
-        dots_to_gaps(wave, wave * kBKV, row_max, raw_max_bf, true, cache[0]);
+        dots_to_gaps(wave, wave * kBKV, row_max, raw_max_bf, !kFoldScale, cache[0]);
         tile_exp(cache[0], slow_div || tile_needs_mask(wave * kBKV));
       } else {
 #pragma unroll
@@ -592,7 +604,7 @@ attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         if (t >= active) continue;
-        dots_to_gaps(t, t * kBKV, row_max, raw_max_bf, true, cache[t]);
+        dots_to_gaps(t, t * kBKV, row_max, raw_max_bf, !kFoldScale, cache[t]);
         tile_exp(cache[t], slow_div || tile_needs_mask(t * kBKV));
 #pragma unroll
         for (int kb32 = 0; kb32 < 2; ++kb32)
@@ -603,7 +615,7 @@ attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
       sweep(natural, false, active, [&](int buf, int kb) {
         const int k0 = kb * kBKV;
         f32x16 s[2];
-        tile_gaps(buf, k0, row_max, raw_max_bf, true, s);
+        tile_gaps(buf, k0, row_max, raw_max_bf, !kFoldScale, s);
         tile_exp(s, slow_div || tile_needs_mask(k0));
 #pragma unroll
         for (int kb32 = 0; kb32 < 2; ++kb32)
@@ -727,7 +739,7 @@ attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const float e = have_e ? s[kb32][r]
-                          : BLOCK_ORDER ? __builtin_amdgcn_exp2f(s[kb32][r] * c_exp) : expf_nonpos(s[kb32][r]);
+                          : BLOCK_ORDER ? __builtin_amdgcn_exp2f(s[kb32][r] * c_exp) : exp_gap(s[kb32][r]);
           float p;
           if constexpr (BLOCK_ORDER) {
             p = e * inv_sum;
@@ -743,7 +755,7 @@ attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
       for (int kb32 = 0; kb32 < 2; ++kb32) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const float e = have_e ? s[kb32][r] : expf_nonpos(s[kb32][r]);
+          const float e = have_e ? s[kb32][r] : exp_gap(s[kb32][r]);
           pf[kb32 * 2 + (r >> 3)][r & 7] = static_cast<__bf16>(e / row_sum);
         }
       }
@@ -785,16 +797,29 @@ attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
 #pragma unroll
     for (int t = 0; t < 2; ++t)
       if (t < active) pv_body(t, cache[t], true);
+  } else if constexpr (!BLOCK_ORDER) {
+    // One loop per division form (fixed for the row): with the choice inside
+    // the loop the two paths' P.V chains left the accumulators in different
+    // registers, copied back every tile.
+    if (!slow_div) {
+      sweep(natural, true, active, [&](int buf, int kb) {
+        f32x16 s[2];
+        tile_gaps(buf, kb * kBKV, row_max, raw_max_bf, !kFoldScale, s);
+        tile_exp(s, tile_needs_mask(kb * kBKV));
+        pv_body(buf, s, true);
+      });
+    } else {
+      sweep(natural, true, active, [&](int buf, int kb) {
+        f32x16 s[2];
+        tile_gaps(buf, kb * kBKV, row_max, raw_max_bf, !kFoldScale, s);
+        pv_body(buf, s, false);
+      });
+    }
   } else {
     sweep(natural, true, active, [&](int buf, int kb) {
       f32x16 s[2];
-      tile_gaps(buf, kb * kBKV, row_max, raw_max_bf, !BLOCK_ORDER, s);
-      if (!BLOCK_ORDER && !slow_div) {
-        tile_exp(s, tile_needs_mask(kb * kBKV));
-        pv_body(buf, s, true);
-      } else {
-        pv_body(buf, s, false);
-      }
+      tile_gaps(buf, kb * kBKV, row_max, raw_max_bf, false, s);
+      pv_body(buf, s, false);
     });
   }
 

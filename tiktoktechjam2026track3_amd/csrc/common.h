@@ -91,6 +91,34 @@ __device__ __forceinline__ float expf_nonpos(float x) {
   return (x < __uint_as_float(0xc2ce8ed0u)) ? 0.f : r;  // -103.27893
 }
 
+// expf_nonpos(g * s) for a power-of-two s, without forming g * s: s is folded
+// into the two log2(e) constants (s * l2e and s * l2e_lo are exact), so the
+// rounded product x * l2e and both fma's see the same exact real values as
+// with x = g * s, and return the same bits.  (g * s itself is exact for the
+// softmax gaps, differences of two bf16 values, even as a subnormal: their
+// spacing is at least 2^-133.)  Callers pass the folded constants
+// (expf_scaled_consts) and the clamp bound -103.27893 / s.
+struct ExpfScaled {
+  float l2e, l2e_lo, clamp;
+};
+__device__ __forceinline__ ExpfScaled expf_scaled_consts(float s) {
+  return ExpfScaled{__uint_as_float(0x3fb8aa3bu) * s, __uint_as_float(0x32a5705fu) * s,
+                    __uint_as_float(0xc2ce8ed0u) / s};
+}
+__device__ __forceinline__ float expf_nonpos_scaled_unclamped(float g, const ExpfScaled& c) {
+#pragma clang fp contract(off)
+  const float ph = g * c.l2e;
+  float pl = __builtin_fmaf(g, c.l2e, -ph);
+  pl = __builtin_fmaf(g, c.l2e_lo, pl);
+  const float n = __builtin_rintf(ph);
+  const float f = (ph - n) + pl;
+  return __builtin_amdgcn_ldexpf(__builtin_amdgcn_exp2f(f), static_cast<int>(n));
+}
+__device__ __forceinline__ float expf_nonpos_scaled(float g, const ExpfScaled& c) {
+  const float r = expf_nonpos_scaled_unclamped(g, c);
+  return (g < c.clamp) ? 0.f : r;
+}
+
 // Exact-erf GELU in fp32: 0.5 * x * (1 + erf(x / sqrt(2))).
 __device__ __forceinline__ float gelu_erf(float x) {
   return 0.5f * x * (1.0f + erff(x * 0.70710678118654752440f));
