@@ -7,6 +7,8 @@ the same device, and the candidate runs the C-ABI path.  The gate is the build's
 bf16 tolerance: strict |d| < 1e-2 OR |d| < 1.6e-2 |ref| for every element.
 """
 
+import time
+
 import pytest
 import torch
 
@@ -140,10 +142,10 @@ def test_encoder_parity_second_trial_c4(device):
     assert result["passed"], result
 
 
-# Sampled c5 sequences: the first, a middle one, two whose element offsets pass
+# Every c5 sequence is checked: among them those whose element offsets pass
 # 2^31 (activations and head-major Q/K beyond sequence 20), and the last, whose
 # final ~18K rows are the library's stream-K tail tiles.
-C5_SEQUENCES = (0, 16, 24, 30, 31)
+C5_SEQUENCES = tuple(range(32))
 
 
 def _c5_sampled(device, causal: bool):
@@ -155,14 +157,17 @@ def _c5_sampled(device, causal: bool):
     name = "case 14 (causal c5)" if causal else "c5"
     with torch.inference_mode():
         x, mask = generate_random_case(cfg, device, torch.bfloat16, spec.seed, spec.padding_ratio, 1.0)
-        out = candidate(x, mask)
+        t0 = time.perf_counter()
+        picked = candidate(x, mask)[list(C5_SEQUENCES)]
         torch.cuda.synchronize()
-        print(f"[{name}] candidate forward done, finite={bool(torch.isfinite(out).all())}", flush=True)
-        picked = out[list(C5_SEQUENCES)].clone()
-        del out
+        t1 = time.perf_counter()
+        print(f"[{name}] candidate forward done in {t1 - t0:.1f} s, finite={bool(torch.isfinite(picked).all())}",
+              flush=True)
         candidate._hip.workspace = None  # room for the oracle's full-batch activations
         torch.cuda.empty_cache()
         ref = encoder_forward_sequences(sd, x, C5_SEQUENCES, causal, cfg.num_heads, cfg.num_layers)
+        torch.cuda.synchronize()
+        print(f"[{name}] oracle done in {time.perf_counter() - t1:.1f} s", flush=True)
     results = []
     for i, b in enumerate(C5_SEQUENCES):
         result = compare(ref[i], picked[i], RTOL, ATOL)
@@ -180,8 +185,8 @@ def test_encoder_parity_c5_sampled_sequences(device):
     oracle recomputes the sampled sequences over all layers, with its Linear
     layers on the whole [3.2M, 1024] batch as the reference runs them and its
     attention walking equal 1000-row query blocks (scores are never
-    materialised for more rows than that).  Every sampled sequence is held to
-    the strict gate."""
+    materialised for more rows than that).  All 32 sequences are held to the
+    strict gate."""
     for b, result, _ in _c5_sampled(device, causal=False):
         assert result["passed"], (b, result)
 
@@ -189,8 +194,8 @@ def test_encoder_parity_c5_sampled_sequences(device):
 @pytest.mark.slow
 def test_encoder_parity_case14_causal_c5_sampled_sequences(device):
     """The reference's official case 14 (cases.py:56): c5's shape with a causal
-    mask, which ran out of memory on the reference's GPU.  Same sampling and
-    strict gate as c5."""
+    mask, which ran out of memory on the reference's GPU.  All 32 sequences,
+    strict gate, as for c5."""
     for b, result, _ in _c5_sampled(device, causal=True):
         assert result["passed"], (b, result)
 
