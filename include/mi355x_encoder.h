@@ -147,7 +147,9 @@ int enc_qkv_proj_bf16(const void* x, const void* weight, const void* bias,
  * bit for bit as the reference computes them with torch on ROCm (the softmax
  * max/sum/divide follow torch's reduction order), by sweeping the keys three
  * times (row max, row sum, probabilities + P.V).  seq_len above 2048 must be
- * a multiple of 4.
+ * a multiple of 4, and one head's K (seq_len * head_dim) and V^T
+ * (head_dim * round_up(seq_len, 8)) must each stay under 4 GiB (the tile
+ * loads use 32-bit offsets inside a head); ENC_ERR_UNSUPPORTED otherwise.
  * Key j is excluded when causal and j > i, when kv_len is non-null and
  * j >= kv_len[b] (prefix padding), or when key_mask is non-null and
  * key_mask[b, j] == 0.  With kv_len, query rows i >= kv_len[b] are padding and
@@ -185,7 +187,9 @@ int enc_attention_online_fwd_bf16(const void* q, const void* k, const void* v_t,
  * reference; for test suites): adds to *mismatches (a device uint32 the
  * caller zeroes) the number of float bit patterns in [lo_bits, hi_bits]
  * (non-positive floats, e.g. 0x80000000 .. 0xc2d00000 = -0 .. -104) where the
- * exact attention's inlined exp differs from the device library's expf. */
+ * exact attention's inlined exp differs from the device library's expf, plus
+ * those where its form with the scale 1/8 folded into the constants,
+ * evaluated on 8x, differs from expf(x). */
 int enc_selfcheck_expf(uint32_t lo_bits, uint32_t hi_bits, uint32_t* mismatches,
                        void* stream);
 

@@ -23,17 +23,23 @@ mask_lengths_kernel(const uint8_t* __restrict__ mask, int64_t S, int32_t* __rest
 }
 
 // Compares expf_nonpos with the device library's expf on every float bit
-// pattern in [lo, hi] (unsigned order; pass patterns of non-positive floats).
+// pattern in [lo, hi] (unsigned order; pass patterns of non-positive floats),
+// and the scale-folded form the short-row attention uses with its scale 1/8
+// (head dim 64): expf_nonpos_scaled(8x) against expf(x).  Each mismatch of
+// either form counts once.
 __global__ void __launch_bounds__(256)
 expf_check_kernel(uint32_t lo, uint32_t hi, uint32_t* __restrict__ mismatches) {
   const uint64_t per_block = 256ull * 64ull;
   const uint64_t first = lo + static_cast<uint64_t>(blockIdx.x) * per_block + threadIdx.x;
+  const ExpfScaled eighth = expf_scaled_consts(0.125f);
   uint32_t bad = 0;
   for (int i = 0; i < 64; ++i) {
     const uint64_t bits = first + static_cast<uint64_t>(i) * 256ull;
     if (bits > hi) break;
     const float x = __uint_as_float(static_cast<uint32_t>(bits));
-    bad += __float_as_uint(expf_nonpos(x)) != __float_as_uint(expf(x));
+    const uint32_t ref = __float_as_uint(expf(x));
+    bad += __float_as_uint(expf_nonpos(x)) != ref;
+    bad += __float_as_uint(expf_nonpos_scaled(x * 8.0f, eighth)) != ref;
   }
   if (bad) atomicAdd(mismatches, bad);
 }
