@@ -77,6 +77,55 @@ __global__ void gelu_ready_kernel() {
   __hip_atomic_store(&g_gelu_ready, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// The wide kernel's GELU epilogue reads a compact copy of the table from LDS:
+// for each sign, the bf16 magnitudes a = bits & 0x7fff in [kGeluLo, kGeluHi]
+// (|x| from 2.4e-4 to 5.53; 7.2 KiB for both signs, which leaves two 256x128
+// workgroups per CU room).  Outside that range the values follow from x
+// itself, as torch's GELU of every bf16 pattern shows (checked exhaustively):
+//   a < kGeluLo:  bf16(0.5 x)  (erf(x / sqrt 2) is below half an ulp of 1);
+//   a > kGeluHi:  x for x > 0, -0 for x < 0, the canonical NaN 0x7fc0 for
+//                 NaN inputs and for -inf (-inf * 0).
+// The table region is filled from g_gelu_table's two slices (the entries for
+// a positive x are x itself from 2.77 on).  A pass whose eight values all lie
+// in the range (nearly every pass for activations of unit scale) does only the
+// lookups; otherwise the pass evaluates the rules above per value.
+constexpr uint32_t kGeluLo = 0x3980u;
+constexpr uint32_t kGeluHi = 0x40b1u;
+constexpr int kGeluSpan = static_cast<int>(kGeluHi - kGeluLo + 1);  // entries per sign
+static_assert(kGeluSpan % 2 == 0 && kGeluLo % 2 == 0, "whole 4-byte words per slice");
+
+// GELU of one bf16 pattern u through the compact table (any u)
+__device__ __forceinline__ uint32_t gelu_compact(const bf16_t* tab, uint32_t u) {
+  const uint32_t a = u & 0x7fffu, s = u >> 15;
+  const uint32_t c = min(max(a, kGeluLo), kGeluHi);
+  const uint32_t t = tab[s * kGeluSpan + (c - kGeluLo)];
+  const uint32_t half = f32_to_bf16(__uint_as_float(u << 16) * 0.5f);
+  const uint32_t big = (a + s > 0x7f80u) ? 0x7fc0u : (s != 0u ? 0x8000u : u);
+  return a < kGeluLo ? half : (a > kGeluHi ? big : t);
+}
+
+// 8 GELU outputs of 8 bf16 values (two per word, low half first)
+__device__ __forceinline__ u32x4 gelu8_lds(const bf16_t* tab, u32x4 v) {
+  uint32_t u[8];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    u[2 * e] = v[e] & 0xffffu;
+    u[2 * e + 1] = v[e] >> 16;
+  }
+  bool in_range = true;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) in_range = in_range && (u[e] & 0x7fffu) - kGeluLo <= kGeluHi - kGeluLo;
+  uint32_t g[8];
+  if (__builtin_amdgcn_ballot_w64(!in_range) == 0) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) g[e] = tab[(u[e] >> 15) * kGeluSpan + ((u[e] & 0x7fffu) - kGeluLo)];
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) g[e] = gelu_compact(tab, u[e]);
+  }
+  return u32x4{g[0] | (g[1] << 16), g[2] | (g[3] << 16), g[4] | (g[5] << 16), g[6] | (g[7] << 16)};
+}
+
 
 template <int EPI>
 __device__ __forceinline__ void store_row_major(const GemmEpilogueArgs& ep, int N, int row,
@@ -409,21 +458,15 @@ struct BigTile {
 template <int EPI>
 __device__ __forceinline__ void finish8(const GemmEpilogueArgs& ep, int N, int row, int col, u32x4 v,
                                         u32x4 r = u32x4{0u, 0u, 0u, 0u}, bool keep = true,
-                                        bool gelu_table = false) {
+                                        bool gelu_table = false, const bf16_t* gelu_tab = nullptr) {
   const int64_t idx = static_cast<int64_t>(row) * N + col;
   u32x4 w;
   if constexpr (EPI == kEpiBias) {
     w = v;
   } else if constexpr (EPI == kEpiBiasGelu) {
     if (gelu_table) {
-      // the table entry of a bf16 pattern is the erf GELU of that value
-      uint32_t g[8];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        g[2 * e] = g_gelu_table[v[e] & 0xffffu];
-        g[2 * e + 1] = g_gelu_table[v[e] >> 16];
-      }
-      w = u32x4{g[0] | (g[1] << 16), g[2] | (g[3] << 16), g[4] | (g[5] << 16), g[6] | (g[7] << 16)};
+      // the compact table in LDS (gelu8_lds) gives the erf GELU of each value
+      w = gelu8_lds(gelu_tab, v);
     } else {
       float g[8];
 #pragma unroll
@@ -455,7 +498,11 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
                 GemmEpilogueArgs ep) {
   using T = BigTile<BM, BN, BK, NS>;
   constexpr int RM = T::kRM, RN = T::kRN;
-  __shared__ __attribute__((aligned(16))) bf16_t smem[T::kSmem];
+  // GELU products append the compact GELU table (2 kGeluSpan entries) and one
+  // word for the workgroup's table verdict
+  constexpr int kGeluLds = EPI == kEpiBiasGelu ? 2 * kGeluSpan + 2 : 0;
+  static_assert((T::kSmem + kGeluLds) * 2 * OCC <= kLdsLimitBytes, "LDS budget for OCC workgroups per CU");
+  __shared__ __attribute__((aligned(16))) bf16_t smem[T::kSmem + kGeluLds];
 
   const int tiles_m = (M + BM - 1) / BM;
   const int tiles_n = N / BN;
@@ -685,6 +732,26 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
     for (int p = 0; p < kDepth; ++p) load_residual(p, res[p], keep[p]);
   }
   bf16_t* sc = smem;  // every wave passed the last barrier: the stages are free
+  // GELU: the compact table's words are requested now, so their latency
+  // overlaps the staging below, and written to LDS before the staging
+  // barrier, together with thread 0's reading of the table's ready flag.
+  // After the barrier every wavefront takes that one verdict, so the whole
+  // workgroup either reads the LDS table or evaluates the erf.  (The words
+  // are read and written either way; before the table is filled they are
+  // never used.)
+  bf16_t* gelu_tab = smem + T::kSmem;
+  constexpr int kGeluWords = kGeluSpan;  // 4-byte words of both slices
+  constexpr int kGeluWordsPerThread = (kGeluWords + kThreads - 1) / kThreads;
+  uint32_t gelu_words[EPI == kEpiBiasGelu ? kGeluWordsPerThread : 1];
+  if constexpr (EPI == kEpiBiasGelu) {
+#pragma unroll
+    for (int i = 0; i < kGeluWordsPerThread; ++i) {
+      const int w = tid + i * kThreads;  // word w of the LDS table
+      const int half_words = kGeluSpan / 2;
+      const uint32_t src = (w < half_words ? kGeluLo : 0x8000u + kGeluLo) + 2u * (w % half_words);
+      if (w < kGeluWords) gelu_words[i] = *reinterpret_cast<const uint32_t*>(&g_gelu_table[src]);
+    }
+  }
 #pragma unroll
   for (int j = 0; j < RN; ++j) {
 #pragma unroll
@@ -705,7 +772,17 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
 #pragma unroll
     for (int p = 0; p < kDepth; ++p) load_residual(p, res[p], keep[p]);
   }
+  if constexpr (EPI == kEpiBiasGelu) {
+#pragma unroll
+    for (int i = 0; i < kGeluWordsPerThread; ++i) {
+      const int w = tid + i * kThreads;
+      if (w < kGeluWords) reinterpret_cast<uint32_t*>(gelu_tab)[w] = gelu_words[i];
+    }
+    if (tid == 0) reinterpret_cast<uint32_t*>(gelu_tab)[kGeluWords] = gelu_flag;
+  }
   __syncthreads();
+  const bool table =
+      EPI == kEpiBiasGelu && __builtin_amdgcn_readfirstlane(reinterpret_cast<const uint32_t*>(gelu_tab)[kGeluWords]) != 0;
   // Every row of the tile is in range (all tiles but the last tile row): the
   // passes then run without a per-row branch, so the compiler can batch their
   // LDS reads and stores.  Uniform.
@@ -724,7 +801,7 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
           if constexpr (kResidual) {
             finish8<EPI>(ep, N, row, n0 + c8, v, res[p % kDepth], keep[p % kDepth]);
           } else {
-            finish8<EPI>(ep, N, row, n0 + c8, v, u32x4{0u, 0u, 0u, 0u}, true, gelu_table);
+            finish8<EPI>(ep, N, row, n0 + c8, v, u32x4{0u, 0u, 0u, 0u}, true, gelu_table, gelu_tab);
           }
         }
         if constexpr (kResidual) {
@@ -732,10 +809,9 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
         }
       }
     };
-    // One verdict per wavefront (the flag only ever turns on).  The GELU
-    // keeps the per-row branch on full tiles too: batched without it, the
-    // table's gathers ran 1-3% slower (32768x4096x1024, 409600x1024x1024).
-    const bool table = EPI == kEpiBiasGelu && __builtin_amdgcn_readfirstlane(gelu_flag) != 0;
+    // One verdict per workgroup (above).  The GELU keeps the per-row branch
+    // on full tiles too (batched without it, the table's global gathers this
+    // epilogue used before the LDS table ran 1-3% slower).
     if (table) {
       passes(true, false);
     } else if (EPI != kEpiBiasGelu && full) {
