@@ -700,7 +700,12 @@ attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
     sweep(resmajor, false, nkb, [&](int buf, int kb) {
       const int k0 = kb * kBKV;
       const int r = kb & 31;
-      while (cur_res < r) finish_residue();  // uniform
+      // Every residue below min(32, nkb) owns a tile, so in residue-major
+      // order the next tile is either the current residue's or the next
+      // one's: at most one residue finishes here (an `if`, not a loop, which
+      // spares the register copies a loop-carried accumulator costs); the
+      // residues with no tile finish after the sweep.
+      if (cur_res < r) finish_residue();  // uniform
       if (CAUSAL && k0 > wq_last) return;
       f32x16 s[2];
       tile_gaps(buf, k0, row_max, raw_max_bf, false, s);
