@@ -353,9 +353,14 @@ def test_ffn_fused_is_the_reference_ffn(device, rows, d, f):
 @pytest.mark.parametrize(
     "b,s,d,h",
     [(1, 128, 512, 8), (2, 100, 512, 8), (8, 1024, 1024, 16), (3, 37, 1024, 16), (64, 128, 32, 4), (3, 37, 128, 16),
-     (2, 100, 1024, 4)],
+     (2, 100, 1024, 4), (4, 300, 128, 32), (4, 1024, 128, 32), (40, 40, 1024, 16), (3, 1000, 1024, 8), (2, 4100, 1024, 16)],
 )
 def test_qkv_head_major(device, b, s, d, h):
+    """Head-major Q, K and padded V^T against torch's linear.  The shapes
+    reach every kernel family: the 16-row tiles (few rows or K <= 256), the
+    large tiles with full and partial tile rows, sequences shorter than a
+    tile's row stride (40 x 40) and not a multiple of 8 (4100), and a
+    head_dim of 4 at a shape the large tiles would otherwise take."""
     g = torch.Generator(device=device).manual_seed(b * s + d)
     x = torch.randn(b, s, d, generator=g, device=device).bfloat16()
     w = (torch.randn(3 * d, d, generator=g, device=device) / math.sqrt(d)).bfloat16()

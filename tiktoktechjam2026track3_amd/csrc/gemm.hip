@@ -868,14 +868,55 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
         }
       }
     }
-    // V^T: one channel, 8 consecutive rows (sequence positions).  Thread t
-    // owns channel t % BN of the tile and row groups t / BN, t / BN + kVStep,
-    // ... of 8 rows each.  Element offset of (b, s): b H hd ld + (h hd + d) ld + s.
+    // V^T on full tiles: two adjacent channels (one head: hd is even), 8
+    // consecutive rows (sequence positions).  Thread t owns channels
+    // 2 (t % (BN/2)) and +1, and row groups t / (BN/2), + kVStep2, ... of 8
+    // rows each: one 4-byte LDS read per row gives both channels' values,
+    // and byte permutes split them into one 16-byte V^T store per channel
+    // (half the LDS reads of one channel per thread).  Element offset of
+    // (b, s): b H hd ld + (h hd + d) ld + s.
+    constexpr int kVPairs = BN / 2;
+    static_assert(kThreads % kVPairs == 0 && BM % (8 * (kThreads / kVPairs)) == 0, "channel pairs per thread");
+    constexpr int kVStep2 = kThreads / kVPairs;
+    const int cp = 2 * (tid % kVPairs);
+    const bool v_fast = full && (S & 7) == 0 && (ep.ld_vt & 7) == 0 && 8 * kVStep2 <= S;
+    if (v_fast && (n0 + cp) / D == 2) {
+      const int h = (n0 + cp - 2 * D) / hd;
+      const int d = (n0 + cp - 2 * D) - h * hd;
+      bf16_t* vrow = ep.v_t + (static_cast<int64_t>(h) * hd + d) * ep.ld_vt;
+      const int64_t batch_stride = static_cast<int64_t>(ep.num_heads) * hd * ep.ld_vt;
+      int b, s;
+      locate(m0 + (tid / kVPairs) * 8, b, s);
+      int64_t off = b * batch_stride + s;
+#pragma unroll
+      for (int it = 0; it < BM / (8 * kVStep2); ++it) {
+        const int r8 = (tid / kVPairs + it * kVStep2) * 8;
+        uint32_t w[8];  // row r8 + e: channel cp in the low half, cp + 1 in the high half
+#pragma unroll
+        for (int e = 0; e < 8; ++e) w[e] = *reinterpret_cast<const uint32_t*>(sc + (r8 + e) * T::kLdc + cp);
+        u32x4 lo, hi;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          lo[e] = __builtin_amdgcn_perm(w[2 * e + 1], w[2 * e], 0x05040100u);  // rows 2e, 2e+1 of channel cp
+          hi[e] = __builtin_amdgcn_perm(w[2 * e + 1], w[2 * e], 0x07060302u);  // ... of channel cp + 1
+        }
+        *reinterpret_cast<u32x4*>(vrow + off) = lo;
+        *reinterpret_cast<u32x4*>(vrow + ep.ld_vt + off) = hi;
+        s += 8 * kVStep2;
+        off += 8 * kVStep2;
+        const bool wrap = s >= S;
+        s = wrap ? s - S : s;
+        off = wrap ? off + batch_stride - S : off;
+      }
+    }
+    // V^T otherwise: one channel, 8 consecutive rows.  Thread t owns channel
+    // t % BN of the tile and row groups t / BN, t / BN + kVStep, ... of 8 rows
+    // each.
     static_assert(kThreads % BN == 0, "one channel per thread");
     constexpr int kVStep = kThreads / BN;
     const int cl = tid % BN;
     const int vcol = n0 + cl;
-    if (vcol / D == 2) {
+    if (!v_fast && vcol / D == 2) {
       const int h = (vcol - 2 * D) / hd;
       const int d = (vcol - 2 * D) - h * hd;
       bf16_t* vrow = ep.v_t + (static_cast<int64_t>(h) * hd + d) * ep.ld_vt;
@@ -1590,7 +1631,10 @@ hipError_t gemm_bf16_plain(const bf16_t* A, const bf16_t* W, int64_t M, int64_t 
   if (split == 2 && chunk == 128) return launch_split<2, 128>(A, W, m, n, k, epi, ep, stream);
   const bool residual = epi == kEpiResidualKeep || epi == kEpiResidualZero;
   const bool ep_overlaps = epi == kEpiBiasGelu || (residual && K <= 1024);
-  switch (pick_big_tile(M, N, A, W, ep, ep_overlaps, num_cus)) {
+  // The large-tile head-major epilogue stores 8 channels of one head at a
+  // time (Q, K) and channel pairs (V^T): head_dim must be a multiple of 8.
+  const bool big_ok = epi != kEpiQkvHeadMajor || ep.head_dim % 8 == 0;
+  switch (big_ok ? pick_big_tile(M, N, A, W, ep, ep_overlaps, num_cus) : 0) {
     case 256129: return launch_big<256, 128, 32, 3, 2>(A, W, m, n, k, epi, ep, stream);
     case 256256: return launch_big<256, 256, 32, 4>(A, W, m, n, k, epi, ep, stream);
     case 256128: return launch_big<256, 128, 64, 3>(A, W, m, n, k, epi, ep, stream);
