@@ -325,6 +325,7 @@ def measure_config(name, args, torch, native, reps):
     torch.manual_seed(spec.seed)
     baseline = BaselineTransformer(cfg)
     candidate = UserOptimizedTransformer(cfg)
+    candidate.native_only = True  # a timed figure is never the torch fallback's
     copy_model_weights(baseline, candidate)
     baseline_sd = {k: v.detach().clone() for k, v in baseline.state_dict().items()}
     del baseline

@@ -4,6 +4,11 @@ from pathlib import Path
 
 import pytest
 
+# The parity tests must exercise the native forward: a call it cannot take
+# raises instead of running the native-torch fallback (tests of the fallback
+# itself turn this off per model).
+os.environ.setdefault("ENC_NATIVE_ONLY", "1")
+
 ROOT = Path(__file__).resolve().parent.parent
 if str(ROOT) not in sys.path:
     sys.path.insert(0, str(ROOT))

@@ -346,11 +346,60 @@ def test_online_attention_encoder_stays_close(device):
     assert result["failed"] < 0.01 * result["total"]
 
 
-def test_unsupported_dtype_raises(device):
+def test_native_only_rejects_a_float32_input(device):
     cfg = TransformerConfig(1, 16, 512, 8, 1024, 1, False)
     model = UserOptimizedTransformer(cfg).to(device).eval()
-    with torch.inference_mode(), pytest.raises(NotImplementedError):
+    model.native_only = True
+    with torch.inference_mode(), pytest.raises(NotImplementedError, match="bfloat16"):
         model(torch.randn(1, 16, 512, device=device))
+    assert model.native_calls == 0
+
+
+def test_float32_on_the_gpu_takes_the_logged_torch_fallback(device):
+    # the reference's native fallback for non-BF16 inputs (TECHNICAL_REPORT.md:542-548)
+    cfg = TransformerConfig(2, 24, 512, 8, 1024, 2, True)
+    torch.manual_seed(7)
+    baseline = BaselineTransformer(cfg)
+    candidate = UserOptimizedTransformer(cfg)
+    copy_model_weights(baseline, candidate)
+    baseline = baseline.to(device).eval()
+    candidate = candidate.to(device).eval()
+    candidate.native_only = False
+    x, mask = generate_random_case(cfg, device, torch.float32, 5, 0.5, 1.0)
+    with torch.inference_mode():
+        ref = baseline(x, mask)
+        out = candidate(x, mask)
+    assert candidate.native_calls == 0 and sum(candidate.fallback_calls.values()) == 1
+    assert "bfloat16" in next(iter(candidate.fallback_calls))
+    assert torch.allclose(out, ref, rtol=1e-5, atol=1e-5), float((out - ref).abs().max())
+
+
+def test_grad_enabled_call_records_autograd_history(device):
+    # the kernels record no history: a training call runs the torch ops and
+    # its gradients are the baseline's
+    cfg = TransformerConfig(1, 16, 128, 4, 256, 1, False)
+    torch.manual_seed(3)
+    baseline = BaselineTransformer(cfg)
+    candidate = UserOptimizedTransformer(cfg)
+    copy_model_weights(baseline, candidate)
+    baseline = baseline.to(device=device, dtype=torch.float32)
+    candidate = candidate.to(device=device, dtype=torch.float32)
+    candidate.native_only = False
+    x = torch.randn(1, 16, 128, device=device)
+    out = candidate(x)
+    ref = baseline(x)
+    assert out.requires_grad and out.grad_fn is not None
+    out.float().square().sum().backward()
+    ref.float().square().sum().backward()
+    assert "autograd" in next(iter(candidate.fallback_calls))
+    g_ref = baseline.layers[0].ffn_in.weight.grad
+    g_out = candidate.layers[0].ffn_in.weight.grad
+    assert torch.allclose(g_out, g_ref, rtol=1e-4, atol=1e-5)
+    # the same module under inference mode takes the native forward again
+    candidate = candidate.to(dtype=torch.bfloat16).eval()
+    with torch.inference_mode():
+        candidate(x.bfloat16())
+    assert candidate.native_calls == 1
 
 
 def test_general_mask_parity(device):

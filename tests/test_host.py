@@ -196,6 +196,36 @@ def test_native_path_rejects_shapes_the_kernels_do_not_cover():
         model._check_native_supported(torch.zeros(1, 8, 128))
 
 
+def test_dispatch_rule_autograd_dtype_and_native_only():
+    # the native forward runs only where every reference route would run its
+    # custom kernels (no autograd history, BF16, a covered shape); the rest
+    # takes the logged torch fallback, or raises under native_only
+    config = TransformerConfig(1, 8, 128, 4, 128, 1, False)
+    model = UserOptimizedTransformer(config)
+    x = torch.randn(1, 8, 128).bfloat16()
+    with torch.no_grad():
+        assert model._fallback_reason(x) is None
+        assert "bfloat16" in model._fallback_reason(x.float())
+    assert "autograd" in model._fallback_reason(x)  # grad enabled, parameters require grad
+    for p in model.parameters():
+        p.requires_grad_(False)
+    assert model._fallback_reason(x) is None
+    assert "autograd" in model._fallback_reason(x.float().requires_grad_())
+    model = model.bfloat16().eval()
+    model.native_only = True
+    with pytest.raises(UnsupportedShapeError, match="native_only"):
+        model._forward_fallback(x, None, "a reason")
+    model.native_only = False
+    with torch.inference_mode():
+        out = model._forward_fallback(x, None, "a reason")
+        out2 = model._forward_fallback(x, None, "a reason")
+        ref = model._forward_eager(x, None)
+    assert torch.equal(out, ref) and torch.equal(out2, ref)
+    assert model.fallback_calls == {"a reason": 2} and model.native_calls == 0
+    # the test session runs strict (tests/conftest.py)
+    assert UserOptimizedTransformer.native_only
+
+
 # --------------------------------------------------------------- profiling ----
 
 def _write_csv(path: Path, header, rows):

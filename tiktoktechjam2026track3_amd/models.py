@@ -17,14 +17,26 @@ Candidate: on CPU it runs the same op sequence as the baseline (the reference's
 CPU fallback contract, tests/test_models.py:30-67).  On a HIP device with bf16
 tensors the whole forward is one call into libmi355x_encoder.so
 (``enc_encoder_forward_bf16``); small shapes are captured once into a HIP graph
-and replayed (models.py:1051-1118, 1163-1239).  Any other dtype on the GPU, or a
-shape the kernels do not support, raises ``UnsupportedShapeError``; there is no
-silent fallback.
+and replayed (models.py:1051-1118, 1163-1239).
+
+What the kernels do not cover takes the reference's "baseline-compatible native
+fallback" (TECHNICAL_REPORT.md:542-548; every custom route in models.py is
+gated on ``torch.is_inference_mode_enabled() and not torch.is_grad_enabled()``
+and on its validated shapes, e.g. models.py:169-170, 989, 1073): a float16 or
+float32 input on the GPU, a shape outside the kernels' limits, or a call that
+records autograd history (grad enabled and the input or a parameter requires
+grad) runs the same op sequence as the CPU path, on the GPU, with torch's
+autograd.  The first call for each reason prints one ``[optimized] fallback``
+line, and ``fallback_calls`` counts them per reason.  A missing or unloadable
+native library is never a reason: it raises.  ``native_only = True`` (or
+``ENC_NATIVE_ONLY=1`` in the environment) turns every fallback into
+``UnsupportedShapeError``; the GPU parity tests and the bench run that way.
 """
 
 from __future__ import annotations
 
 import copy
+import os
 import weakref
 from typing import Dict, List, Optional, Tuple
 
@@ -63,7 +75,8 @@ PACK_MIN_ROWS = 1024
 
 
 class UnsupportedShapeError(NotImplementedError):
-    """The native kernels do not cover this shape/dtype; no fallback is taken."""
+    """The native kernels do not cover this shape/dtype/mode (raised by the
+    shape check, and by ``forward`` when ``native_only`` forbids the fallback)."""
 
 
 def _attention_core(
@@ -392,6 +405,8 @@ class UserOptimizedTransformer(BaselineTransformer):
     """
 
     online_attention: bool = False
+    # Raise instead of taking the native-torch fallback (see the module header).
+    native_only: bool = os.environ.get("ENC_NATIVE_ONLY", "") not in ("", "0")
 
     def __init__(self, config: TransformerConfig) -> None:
         nn.Module.__init__(self)
@@ -424,6 +439,9 @@ class UserOptimizedTransformer(BaselineTransformer):
         self._cuda_graph_final_norm = False
         self._cuda_graph_row_mask: Optional[torch.Tensor] = None
         self._mask_memo = _MaskClassMemo()
+        # GPU calls by path: through libmi355x_encoder.so, and per fallback reason
+        self.native_calls = 0
+        self.fallback_calls: Dict[str, int] = {}
 
     # ---- mask classification (memoised per tensor version) ----
 
@@ -724,6 +742,34 @@ class UserOptimizedTransformer(BaselineTransformer):
         graph.replay()
         return self._graph_result()
 
+    # ---- dispatch between the native forward and the torch fallback ----
+
+    def _fallback_reason(self, x: torch.Tensor) -> Optional[str]:
+        """Why a GPU call cannot take the native forward, or None when it can.
+
+        Autograd comes first: the kernels record no history, so a call that
+        would (grad enabled and the input or a parameter requires grad) runs
+        the torch ops, as every reference route does outside inference mode.
+        """
+        if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())):
+            return "autograd: grad is enabled and a tensor requires grad (the kernels record no history)"
+        try:
+            self._check_native_supported(x)
+        except UnsupportedShapeError as error:
+            return str(error)
+        return None
+
+    def _forward_fallback(
+        self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor], reason: str
+    ) -> torch.Tensor:
+        if self.native_only:
+            raise UnsupportedShapeError(f"native_only is set and the native forward cannot run: {reason}")
+        count = self.fallback_calls.get(reason, 0)
+        if count == 0:
+            print(f"[optimized] fallback to native torch ops on {x.device}: {reason}")
+        self.fallback_calls[reason] = count + 1
+        return self._forward_eager(x, valid_token_mask)
+
     # ---- entry point ----
 
     def forward(
@@ -731,14 +777,20 @@ class UserOptimizedTransformer(BaselineTransformer):
         x: torch.Tensor,
         valid_token_mask: Optional[torch.Tensor] = None,
     ) -> torch.Tensor:
+        if x.device.type == "cuda":
+            reason = self._fallback_reason(x)
+            if reason is not None:
+                return self._forward_fallback(x, valid_token_mask, reason)
         if not self._cuda_graph_eligible(x, valid_token_mask):
             if x.device.type != "cuda":
                 return self._forward_eager(x, valid_token_mask)
+            self.native_calls += 1
             mask_kind = MASK_ALL_TRUE
             if valid_token_mask is not None:
                 mask_kind = self._mask_kind(valid_token_mask)
             return self._forward_native(x, valid_token_mask, mask_kind)
 
+        self.native_calls += 1
         mask_kind = MASK_ALL_TRUE
         if valid_token_mask is not None:
             mask_kind = self._mask_kind(valid_token_mask)

@@ -404,6 +404,14 @@ def _run_benchmark_case_with_profile(
         warmup=args.warmup, repeats=args.repeats, rounds=args.benchmark_rounds,
     )
     if device.type == "cuda":
+        # which path the candidate's GPU calls took (the native forward, or the
+        # logged native-torch fallback per reason), so no figure is read as
+        # the kernels' when it was not
+        module = getattr(optimized, "_orig_mod", optimized)
+        performance["candidate_backend"] = {
+            "native_calls": int(getattr(module, "native_calls", 0)),
+            "fallback_calls": dict(getattr(module, "fallback_calls", {})),
+        }
         performance["roofline"] = roofline_summary(config, performance)
         print(f"roofline: {performance['roofline']['fraction_of_bf16_mfma_peak']:.2%} of bf16 MFMA peak")
     if baseline_cpu is not None:

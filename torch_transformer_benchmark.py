@@ -62,7 +62,16 @@ from tiktoktechjam2026track3_amd.runner import (  # noqa: E402
     write_json_result,
     write_matrix_result,
 )
+from tiktoktechjam2026track3_amd.profiling import (  # noqa: E402
+    PROFILE_CANDIDATE_REPLAYS,
+    PROFILE_MAX_CASES,
+    PROFILE_MAX_EVENTS,
+    PROFILE_WARMUP_REPLAYS,
+    profile_candidate,
+    summarize_profile_events,
+)
 from tiktoktechjam2026track3_amd.timing import (  # noqa: E402
+    TimingResult,
     benchmark_models,
     benchmark_once,
     percentile,
@@ -79,7 +88,9 @@ __all__ = [
     "release_case_memory", "resolve_device", "resolve_dtype", "run_benchmark_case",
     "run_encoder_configs", "run_official_matrix", "run_single_case", "settings_metadata",
     "validate_args", "write_json_document", "write_json_result", "write_matrix_result",
-    "benchmark_models", "benchmark_once", "percentile", "warmup_model",
+    "PROFILE_CANDIDATE_REPLAYS", "PROFILE_MAX_CASES", "PROFILE_MAX_EVENTS", "PROFILE_WARMUP_REPLAYS",
+    "profile_candidate", "summarize_profile_events",
+    "TimingResult", "benchmark_models", "benchmark_once", "percentile", "warmup_model",
 ]
 
 
