@@ -81,6 +81,34 @@ int enc_linear_bf16(const void* a, const void* weight, const void* bias,
                     int64_t out_features, int64_t in_features, int32_t epilogue,
                     const uint8_t* row_mask, void* stream);
 
+/* Registers, for the given device, the reduction order that the reference's
+ * nn.Linear (torch.nn.functional.linear, i.e. hipBLASLt on ROCm) uses for the
+ * bf16 product [rows, in_features] x [out_features, in_features]^T, as measured
+ * on that device by the host.  tile_rows == 0 records that no output tile has
+ * its K range split: every product of this shape (and the head-major QKV
+ * projection of three such slices) accumulates K sequentially.  Otherwise the
+ * library's last output tiles of 256 x 256 are a stream-K tail: split is a
+ * row-major [tile_rows, tile_cols] table of the tiles from tile row
+ * first_tile_row to the last (tile_cols = out_features / 256), each entry the
+ * first K index of the tile's second partial sum (a multiple of 32), or 0 for
+ * a tile accumulated in one pass; such a tile is computed as
+ * bf16((P1 + P2) + bias), P1 over K < split and P2 over K >= split.  At most
+ * 1024 entries.  A registration replaces an earlier one for the same shape
+ * and device, and takes precedence over the library's built-in tables (two
+ * shapes, measured on a 256-CU MI355X and used only on such a device).
+ * Host-side state only; safe to call from any thread, not during a call that
+ * runs the same shape.  Replaces what the reference gets implicitly from
+ * hipBLASLt at every nn.Linear call (transformer_benchmark/models.py:30-33,
+ * 724-725): the library picks the split per shape, so the host measures it
+ * (tiktoktechjam2026track3_amd/linear_order.py) and hands it down here. */
+int enc_linear_order_register(int32_t device, int64_t rows, int64_t out_features,
+                              int64_t in_features, int32_t first_tile_row,
+                              int32_t tile_rows, int32_t tile_cols,
+                              const uint16_t* split);
+
+/* Forgets every registered order (all devices). */
+int enc_linear_order_clear(void);
+
 /* Tile-packed copy of an nn.Linear weight W[out_features, in_features] for
  * the wide GEMM kernel: element (n, k) moves to
  *   ((n / P * (in_features / 32) + k / 32) * P + n % P) * 32 + k % 32,

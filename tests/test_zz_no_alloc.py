@@ -25,9 +25,9 @@ def _model(cfg, seed, device):
     return candidate.to(device=device, dtype=torch.bfloat16).eval()
 
 
-def _both(model, x, mask):
+def _both(model, x, mask, rows=None):
     cfg = model.config
-    table, eps, packed = model._native_weights(x.device, x.shape[0] * x.shape[1])
+    table, eps, packed = model._native_weights(x.device, x.shape[0] * x.shape[1] if rows is None else rows)
     kv_len = row_mask = None
     if mask is not None and not bool(mask.all()):
         kv_len = native.mask_lengths(mask)
@@ -62,6 +62,42 @@ def test_noalloc_forward_matches_workspace_forward(device):
         print(f"[noalloc] smaller second call equal={torch.equal(ref2, out2)}", flush=True)
         assert torch.equal(ref2, out2)
         assert torch.all(out2[~mask2] == 0)
+
+
+@pytest.mark.parametrize("packed", [False, True], ids=["plain_weights", "packed_weights"])
+def test_noalloc_forward_at_a_wide_tile_shape(device, packed):
+    """2304 tokens at d_model 1024 / ffn 4096 (a 52 MB workspace, within the
+    64 MiB array): the wide GEMM tiles, the 256 x 256 GELU tile (which keeps
+    three words in scratch), the GELU table and, with packed_weights, the
+    tile-packed weights.  Bitwise against the workspace forward, twice; the
+    second no-allocation call leaves the device's free memory unchanged."""
+    from tiktoktechjam2026track3_amd import linear_order
+
+    cfg = TransformerConfig(1, 2304, 1024, 16, 4096, 1, True)
+    need = native.encoder_workspace_bytes(1, 2304, 1024, 16, 4096)
+    assert need <= native.NOALLOC_SCRATCH_BYTES
+    model = _model(cfg, 11, device)
+    rows = 2304 if packed else 0  # 0 rows: below the packing threshold, plain weights only
+    with torch.inference_mode():
+        linear_order.ensure_encoder(2304, 1024, 4096, device)
+        x, mask = generate_random_case(cfg, device, torch.bfloat16, 12, 0.3, 1.0)
+        ref, out = _both(model, x, mask, rows)
+        assert torch.equal(ref, out)
+        table, eps, used_packed = model._native_weights(device, rows)
+        assert used_packed == packed
+        kv_len = native.mask_lengths(mask)
+        row_mask = mask.contiguous().view(torch.uint8)
+        out2 = torch.full_like(x, float("nan"))
+        torch.cuda.synchronize()
+        free_before = torch.cuda.mem_get_info(device)[0]
+        native.encoder_forward_noalloc(x, out2, table, cfg.num_heads, cfg.ffn_dim, cfg.num_layers, eps,
+                                       cfg.causal, kv_len, None, row_mask, packed_weights=used_packed)
+        torch.cuda.synchronize()
+        free_after = torch.cuda.mem_get_info(device)[0]
+    print(f"[noalloc] wide tiles packed={packed}: equal={torch.equal(ref, out2)}, "
+          f"free memory {free_before} -> {free_after}", flush=True)
+    assert torch.equal(ref, out2)
+    assert free_after == free_before
 
 
 def test_noalloc_rejects_shapes_above_the_scratch_array(device):

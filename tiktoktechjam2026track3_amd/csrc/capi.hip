@@ -243,7 +243,8 @@ int run_encoder_forward(const void* x, void* out, void* workspace, const Encoder
   // need 16-byte aligned weights (all but the QKV projection's).
   // (With more tokens the four launches win: the fused kernel's one workgroup
   // per CU cannot hide its per-slab latency; measured on MI355X.)
-  bool tail_fused = enc::block_tail_supported(D, F) && T <= 8192;
+  bool tail_fused = enc::block_tail_supported(D, F) && T <= 8192 && !enc::gemm_has_split_tail(T, D, D, cus) &&
+                    !enc::gemm_has_split_tail(T, F, D, cus) && !enc::gemm_has_split_tail(T, D, F, cus);
   for (int64_t layer = 0; tail_fused && layer < num_layers; ++layer)
     for (int idx = 0; idx < 12; ++idx)
       tail_fused = tail_fused && (idx == 2 || idx == 3 || reinterpret_cast<uintptr_t>(W(layer, idx)) % 16 == 0);
@@ -341,6 +342,23 @@ extern "C" {
 int enc_version(void) { return (1 << 16) | 1; }
 
 const char* enc_last_error(void) { return g_last_error.c_str(); }
+
+int enc_linear_order_register(int32_t device, int64_t rows, int64_t out_features, int64_t in_features,
+                              int32_t first_tile_row, int32_t tile_rows, int32_t tile_cols, const uint16_t* split) {
+  if (device < 0) return fail(ENC_ERR_INVALID, "linear_order_register: device must be >= 0");
+  if (enc::gemm_order_register(device, rows, out_features, in_features, first_tile_row, tile_rows, tile_cols,
+                               split) != 0)
+    return fail(ENC_ERR_INVALID,
+                "linear_order_register: the table does not fit the shape (out_features % 256 == 0, "
+                "tile_cols == out_features / 256, at most 1024 entries, tiles covering the last rows, "
+                "split points multiples of 32 below in_features)");
+  return ok();
+}
+
+int enc_linear_order_clear(void) {
+  enc::gemm_order_clear();
+  return ok();
+}
 
 int enc_layernorm_bf16(const void* x, const void* gamma, const void* beta, void* y, int64_t rows,
                        int64_t width, float eps, const uint8_t* row_mask, void* stream) {

@@ -22,7 +22,9 @@
 // workgroups round-robin over its 8 XCDs, so the linear id is remapped so each
 // XCD walks a contiguous range of tiles, which are ordered in groups of 8 tile
 // rows so concurrently running tiles share A rows and W columns in that XCD's L2.
+#include <algorithm>
 #include <mutex>
+#include <vector>
 
 #include "common.h"
 #include "kernels.h"
@@ -1313,7 +1315,7 @@ hipError_t launch_big(const bf16_t* A, const bf16_t* W, int M, int N, int K, int
 //   y = bf16(P + bias)                  (s == 0: one pass, as elsewhere)
 // through the usual epilogue.  Only the tail rows run here (0.6% of c5's rows),
 // so the kernel stages operands through registers and LDS plainly.
-constexpr int kTailMaxTiles = 288;
+constexpr int kTailMaxTiles = 1024;  // 2 KiB of kernel arguments
 struct TailSplitArgs {
   int row_begin;   // first row of the tail, a multiple of 256
   int slice_n;     // N of the library product the table describes
@@ -1446,24 +1448,81 @@ gemm_tail_split_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ 
   }
 }
 
-// The stream-K tail table for this product, or null.  The packed QKV
-// projection (N = 3 x slice_n, head-major epilogue) matches too: the reference
-// runs the q, k and v projections as three [M, K] x [slice_n, K]^T products.
-const StreamKTail* find_streamk_tail(int64_t M, int64_t N, int64_t K, int epi) {
-  for (const StreamKTail& t : kStreamKTails)
-    if (t.m == M && t.k == K && (N == t.n || (epi == kEpiQkvHeadMajor && N == 3 * t.n))) return &t;
-  return nullptr;
+// Reduction orders measured on the running device and registered by the host
+// (enc_linear_order_register): per device and library product shape
+// (M, N, K), either "sequential" (no tile of the library's product has its K
+// range split) or a tail table in the StreamKTail layout.  They take
+// precedence over the built-in tables below, which were measured on a 256-CU
+// MI355X and apply only on a device with that many CUs.
+struct RegisteredOrder {
+  int device;
+  int64_t m;
+  int n, k;
+  int first_tile_row, tile_rows, tile_cols;
+  std::vector<uint16_t> split;  // empty: sequential
+};
+std::mutex g_order_mutex;
+std::vector<RegisteredOrder> g_orders;
+
+// What gemm_bf16 uses for one product: no split, or a copy of a tail table.
+struct TailLookup {
+  bool split = false;
+  int64_t m = 0;
+  int n = 0, k = 0;
+  int first_tile_row = 0, tile_rows = 0, tile_cols = 0;
+  uint16_t table[kTailMaxTiles] = {};
+};
+
+// The packed QKV projection (N = 3 x slice_n, head-major epilogue) matches a
+// slice_n entry: the reference runs the q, k and v projections as three
+// [M, K] x [slice_n, K]^T products.
+bool order_matches(int64_t tm, int64_t tn, int64_t tk, int64_t M, int64_t N, int64_t K, int epi) {
+  return tm == M && tk == K && (N == tn || (epi == kEpiQkvHeadMajor && N == 3 * tn));
+}
+
+void lookup_order(int64_t M, int64_t N, int64_t K, int epi, int num_cus, TailLookup* out) {
+  out->split = false;
+  int dev = -1;
+  if (hipGetDevice(&dev) == hipSuccess) {
+    std::lock_guard<std::mutex> guard(g_order_mutex);
+    for (const RegisteredOrder& r : g_orders) {
+      if (r.device != dev || !order_matches(r.m, r.n, r.k, M, N, K, epi)) continue;
+      if (r.split.empty()) return;
+      out->split = true;
+      out->m = r.m;
+      out->n = r.n;
+      out->k = r.k;
+      out->first_tile_row = r.first_tile_row;
+      out->tile_rows = r.tile_rows;
+      out->tile_cols = r.tile_cols;
+      std::copy(r.split.begin(), r.split.end(), out->table);
+      return;
+    }
+  }
+  if (num_cus != kStreamKTablesCUs) return;
+  for (const StreamKTail& t : kStreamKTails) {
+    if (!order_matches(t.m, t.n, t.k, M, N, K, epi)) continue;
+    out->split = true;
+    out->m = t.m;
+    out->n = t.n;
+    out->k = t.k;
+    out->first_tile_row = t.first_tile_row;
+    out->tile_rows = t.tile_rows;
+    out->tile_cols = t.tile_cols;
+    std::copy(t.split, t.split + t.tile_rows * t.tile_cols, out->table);
+    return;
+  }
 }
 
 hipError_t launch_tail_split(const bf16_t* A, const bf16_t* W, int M, int N, int K, int epi,
-                             const StreamKTail& t, const GemmEpilogueArgs& ep, hipStream_t st) {
+                             const TailLookup& t, const GemmEpilogueArgs& ep, hipStream_t st) {
   TailSplitArgs ts;
   ts.row_begin = t.first_tile_row * 256;
   ts.slice_n = t.n;
   ts.tile_cols = t.tile_cols;
   const int entries = t.tile_rows * t.tile_cols;
-  if (entries > kTailMaxTiles) return hipErrorInvalidValue;
-  for (int i = 0; i < kTailMaxTiles; ++i) ts.split[i] = i < entries ? t.split[i] : 0;
+  if (entries > kTailMaxTiles || t.tile_cols * 256 != t.n || N % 128 != 0) return hipErrorInvalidValue;
+  for (int i = 0; i < kTailMaxTiles; ++i) ts.split[i] = i < entries ? t.table[i] : 0;
   const int rows = M - ts.row_begin;
   const dim3 grid(static_cast<uint32_t>((rows + 127) / 128 * (N / 128))), block(kThreads);
   switch (epi) {
@@ -1655,13 +1714,56 @@ hipError_t gemm_bf16(const bf16_t* A, const bf16_t* W, int64_t M, int64_t N, int
                      const GemmEpilogueArgs& ep, int num_cus, hipStream_t stream) {
   // a packed copy must be the one gemm_prepack_weight writes for this shape
   if (ep.w_packed != nullptr && ep.w_packed_rows != gemm_prepack_rows(N, K)) return hipErrorInvalidValue;
-  const StreamKTail* tail = find_streamk_tail(M, N, K, epi);
-  if (tail == nullptr) return gemm_bf16_plain(A, W, M, N, K, epi, ep, num_cus, stream);
+  TailLookup tail;
+  lookup_order(M, N, K, epi, num_cus, &tail);
+  if (!tail.split) return gemm_bf16_plain(A, W, M, N, K, epi, ep, num_cus, stream);
   // rows before the library's stream-K tail as usual, the tail's rows split
-  const int64_t row_begin = static_cast<int64_t>(tail->first_tile_row) * 256;
+  const int64_t row_begin = static_cast<int64_t>(tail.first_tile_row) * 256;
   hipError_t e = gemm_bf16_plain(A, W, row_begin, N, K, epi, ep, num_cus, stream);
   if (e != hipSuccess) return e;
-  return launch_tail_split(A, W, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), epi, *tail, ep, stream);
+  return launch_tail_split(A, W, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), epi, tail, ep, stream);
+}
+
+bool gemm_has_split_tail(int64_t M, int64_t N, int64_t K, int num_cus) {
+  TailLookup tail;
+  lookup_order(M, N, K, kEpiBias, num_cus, &tail);
+  return tail.split;
+}
+
+int gemm_order_register(int device, int64_t M, int64_t N, int64_t K, int first_tile_row, int tile_rows,
+                        int tile_cols, const uint16_t* split) {
+  if (M <= 0 || N <= 0 || K <= 0 || tile_rows < 0 || first_tile_row < 0) return 1;
+  if (tile_rows > 0) {
+    if (split == nullptr || N % 256 != 0 || tile_cols != N / 256 || tile_rows * tile_cols > kTailMaxTiles ||
+        (static_cast<int64_t>(first_tile_row) + tile_rows) * 256 < M ||
+        static_cast<int64_t>(first_tile_row) * 256 >= M)
+      return 1;
+    for (int i = 0; i < tile_rows * tile_cols; ++i)
+      if (split[i] >= K || split[i] % 32 != 0) return 1;
+  }
+  RegisteredOrder r;
+  r.device = device;
+  r.m = M;
+  r.n = static_cast<int>(N);
+  r.k = static_cast<int>(K);
+  r.first_tile_row = first_tile_row;
+  r.tile_rows = tile_rows;
+  r.tile_cols = tile_rows > 0 ? tile_cols : 0;
+  if (tile_rows > 0) r.split.assign(split, split + tile_rows * tile_cols);
+  std::lock_guard<std::mutex> guard(g_order_mutex);
+  for (RegisteredOrder& o : g_orders) {
+    if (o.device == device && o.m == M && o.n == N && o.k == K) {
+      o = std::move(r);
+      return 0;
+    }
+  }
+  g_orders.push_back(std::move(r));
+  return 0;
+}
+
+void gemm_order_clear() {
+  std::lock_guard<std::mutex> guard(g_order_mutex);
+  g_orders.clear();
 }
 
 }  // namespace enc

@@ -58,6 +58,18 @@ hipError_t gemm_bf16(const bf16_t* A, const bf16_t* W, int64_t M, int64_t N, int
 int gemm_prepack_rows(int64_t N, int64_t K);
 hipError_t gemm_prepack_weight(const bf16_t* W, bf16_t* packed, int64_t N, int64_t K, hipStream_t stream);
 
+// Measured reduction orders of the reference's nn.Linear (hipBLASLt) for the
+// current device, keyed by the library product's (M, N, K): tile_rows == 0
+// records that no tile's K range is split; otherwise split[] is a tail table
+// of tile_rows x tile_cols 256 x 256 tiles from first_tile_row (first K index
+// of the second partial sum, 0 for a one-pass tile).  Returns 0, or 1 when
+// the table is inconsistent with the shape.
+int gemm_order_register(int device, int64_t M, int64_t N, int64_t K, int first_tile_row, int tile_rows,
+                        int tile_cols, const uint16_t* split);
+void gemm_order_clear();
+// Whether gemm_bf16 would accumulate some tile of this product in two partials.
+bool gemm_has_split_tail(int64_t M, int64_t N, int64_t K, int num_cus);
+
 // Tile shape the dispatcher picks for (M, N) on a device with num_cus CUs.
 void gemm_pick_tile(int64_t M, int64_t N, int epilogue, int num_cus, int* bm, int* bn);
 // K-split reduction order matching torch.nn.functional.linear for this shape:

@@ -393,6 +393,10 @@ class _HipState:
         self.packed: Optional[torch.Tensor] = None
         self.packed_views: List[torch.Tensor] = []
         self.packed_key: Optional[Tuple[object, ...]] = None
+        # (device, token count) whose nn.Linear reduction orders were checked,
+        # and the reason the native forward cannot reproduce them (or None)
+        self.order_key: Optional[Tuple[object, ...]] = None
+        self.order_reason: Optional[str] = None
 
 
 class UserOptimizedTransformer(BaselineTransformer):
@@ -757,7 +761,28 @@ class UserOptimizedTransformer(BaselineTransformer):
             self._check_native_supported(x)
         except UnsupportedShapeError as error:
             return str(error)
-        return None
+        return self._linear_order_reason(x)
+
+    def _linear_order_reason(self, x: torch.Tensor) -> Optional[str]:
+        """Why the reference's nn.Linear products at this token count cannot be
+        reproduced, or None.  Their reduction order is measured on the device
+        the first time a token count is seen (linear_order.py)."""
+        from . import linear_order
+
+        if x.device.type != "cuda":
+            return None
+        cfg = self.config
+        key = (x.device, x.shape[0] * x.shape[1])
+        state = self._hip
+        if state.order_key != key:
+            reason = None
+            for order in linear_order.ensure_encoder(key[1], cfg.d_model, cfg.ffn_dim, x.device):
+                if not order.representable:
+                    reason = (f"torch's nn.Linear reduces [{order.m}, {order.k}] x [{order.n}, {order.k}]^T "
+                              f"in an order the native GEMM does not reproduce ({order.reason})")
+                    break
+            state.order_key, state.order_reason = key, reason
+        return state.order_reason
 
     def _forward_fallback(
         self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor], reason: str

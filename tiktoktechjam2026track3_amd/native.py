@@ -44,6 +44,8 @@ _F32 = ctypes.c_float
 SIGNATURES = (
     ("enc_version", ctypes.c_int, ()),
     ("enc_last_error", ctypes.c_char_p, ()),
+    ("enc_linear_order_register", ctypes.c_int, (_I32, _I64, _I64, _I64, _I32, _I32, _I32, _VP)),
+    ("enc_linear_order_clear", ctypes.c_int, ()),
     ("enc_layernorm_bf16", ctypes.c_int, (_VP, _VP, _VP, _VP, _I64, _I64, _F32, _VP, _VP)),
     ("enc_linear_bf16", ctypes.c_int, (_VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I32, _VP, _VP)),
     ("enc_prepack_weight_bf16", ctypes.c_int, (_VP, _VP, _I64, _I64, _VP)),
@@ -144,6 +146,15 @@ def _stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
+def _ensure_order(rows: int, n: int, k: int, device: torch.device) -> None:
+    """Make sure the library knows how the reference's nn.Linear reduces this
+    shape on this device (measured once per shape, linear_order.py), and
+    refuse a shape whose order it cannot reproduce."""
+    from . import linear_order
+
+    linear_order.require(linear_order.ensure(rows, n, k, device))
+
+
 def _require(tensor: torch.Tensor, name: str, dtype: torch.dtype) -> None:
     if tensor.device.type != "cuda":
         raise ValueError(f"{name} must be a CUDA (HIP) tensor")
@@ -227,6 +238,7 @@ def linear(
     if a.shape[-1] != k or bias.numel() != n:
         raise ValueError(f"shape mismatch: a {tuple(a.shape)}, weight {tuple(weight.shape)}")
     rows = a.numel() // k
+    _ensure_order(rows, n, k, a.device)
     out = torch.empty((*a.shape[:-1], n), device=a.device, dtype=a.dtype) if out is None else out
     if residual is not None:
         _require(residual, "residual", torch.bfloat16)
@@ -277,6 +289,8 @@ def ffn(
     if residual.shape != h.shape:
         raise ValueError("residual must have h's shape")
     rows = h.numel() // d
+    _ensure_order(rows, f, d, h.device)
+    _ensure_order(rows, d, f, h.device)
     out = torch.empty_like(h) if out is None else out
     hidden = torch.empty((rows, f), device=h.device, dtype=h.dtype) if hidden is None else hidden
     if hidden.numel() < rows * f or not hidden.is_contiguous():
@@ -306,6 +320,7 @@ def qkv_proj(
     batch, seq_len, d_model = x.shape
     if tuple(weight.shape) != (3 * d_model, d_model) or bias.numel() != 3 * d_model:
         raise ValueError("qkv weight must be [3*d_model, d_model] with a [3*d_model] bias")
+    _ensure_order(batch * seq_len, d_model, d_model, x.device)
     hd = d_model // num_heads
     q = torch.empty((batch, num_heads, seq_len, hd), device=x.device, dtype=x.dtype)
     k = torch.empty_like(q)
@@ -434,6 +449,10 @@ def encoder_forward(
     """
     flags = _forward_flags(online_attention, final_norm, packed_weights, weight_table, num_layers)
     batch, seq_len, d_model = x.shape
+    from . import linear_order
+
+    for order in linear_order.ensure_encoder(batch * seq_len, d_model, ffn_dim, x.device):
+        linear_order.require(order)
     table = ctypes.cast(weight_table.data_ptr(), ctypes.c_void_p)
     _check(
         "enc_encoder_forward_bf16",
@@ -465,9 +484,15 @@ def encoder_forward_noalloc(
     """enc_encoder_forward_bf16_noalloc: the encoder forward over the library's
     own static scratch array (no workspace argument, no device allocation).
     Calls that overlap on one GPU share that array and must not run
-    concurrently."""
+    concurrently.  The reduction orders of the three product shapes must be
+    known already (linear_order.ensure_encoder, or an earlier workspace
+    forward at the same shape): measuring them allocates."""
     flags = _forward_flags(online_attention, final_norm, packed_weights, weight_table, num_layers)
     batch, seq_len, d_model = x.shape
+    from . import linear_order
+
+    for order in linear_order.known_encoder_orders(batch * seq_len, d_model, ffn_dim, x.device):
+        linear_order.require(order)
     table = ctypes.cast(weight_table.data_ptr(), ctypes.c_void_p)
     _check(
         "enc_encoder_forward_bf16_noalloc",
