@@ -109,6 +109,16 @@ int enc_linear_order_register(int32_t device, int64_t rows, int64_t out_features
 /* Forgets every registered order (all devices). */
 int enc_linear_order_clear(void);
 
+/* Test hook, no counterpart in the reference (for tests that must tell the
+ * GELU epilogue's two paths apart; they give the same bits by design).  On
+ * the current device, enqueued on stream after the GELU table's fill:
+ * ready >= 0 sets the table's ready flag (0 makes every GELU epilogue of the
+ * wide GEMM evaluate the erf, 1 lets it read the table); entry in [0, 65535]
+ * overwrites that bf16 pattern's table entry with value in [0, 65535], or
+ * recomputes it when value is -1.  Not for production use: a changed entry
+ * changes the GELU of every later product until it is restored. */
+int enc_debug_gelu_table(int32_t ready, int32_t entry, int32_t value, void* stream);
+
 /* Tile-packed copy of an nn.Linear weight W[out_features, in_features] for
  * the wide GEMM kernel: element (n, k) moves to
  *   ((n / P * (in_features / 32) + k / 32) * P + n % P) * 32 + k % 32,

@@ -181,6 +181,39 @@ def test_gelu_epilogue_every_bf16_input(device, packed):
     assert bool((same | nan_ref).all()), int((~(same | nan_ref)).sum())
 
 
+def test_gelu_epilogue_table_and_erf_paths(device):
+    """Both paths of the wide kernel's GELU epilogue, told apart: with one
+    table entry overwritten (x = 1.0), the table path returns the planted
+    value for exactly that input; with the ready flag cleared, every input
+    goes through the erf and all 65536 outputs are torch's again.  Both paths
+    are checked over every bf16 input."""
+    m, n, k = 1024, 65536, 64
+    a = torch.randn(m, k, device=device).bfloat16()
+    w = torch.zeros(n, k, device=device, dtype=torch.bfloat16)
+    bias = torch.arange(n, device=device, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    ref = F.gelu(F.linear(a, w, bias), approximate="none")
+    nan_ref = torch.isnan(ref)
+
+    def mismatches(out):
+        same = out.view(torch.int16) == ref.view(torch.int16)
+        return ~(same | (nan_ref & torch.isnan(out)))
+
+    one, planted = 0x3F80, 0x1234
+    try:
+        native.debug_gelu_table(device, entry=one, value=planted)
+        out = native.linear(a, w, bias, native.ENC_EPI_BIAS_GELU)
+        bad = mismatches(out)
+        assert bool(bad[:, one].all()) and bool((out[:, one].view(torch.int16) == planted).all())
+        assert int(bad.sum()) == m, "only the planted entry differs: the table path ran"
+        native.debug_gelu_table(device, ready=0)
+        out = native.linear(a, w, bias, native.ENC_EPI_BIAS_GELU)
+        assert int(mismatches(out).sum()) == 0, "the erf path ignores the table"
+    finally:
+        native.debug_gelu_table(device, ready=1, entry=one, value=-1)
+    out = native.linear(a, w, bias, native.ENC_EPI_BIAS_GELU)
+    assert int(mismatches(out).sum()) == 0
+
+
 @pytest.mark.parametrize("epi", [native.ENC_EPI_BIAS_RESIDUAL_KEEP, native.ENC_EPI_BIAS_RESIDUAL_ZERO])
 @pytest.mark.parametrize("m,n,k", [(100, 512, 512), (8192, 1024, 1024), (1000, 1024, 4096)])
 def test_linear_residual(device, m, n, k, epi):

@@ -360,6 +360,14 @@ int enc_linear_order_clear(void) {
   return ok();
 }
 
+int enc_debug_gelu_table(int32_t ready, int32_t entry, int32_t value, void* stream) {
+  if (ready > 1 || entry > 65535 || value > 65535 || value < -1 || (entry < 0 && value != -1))
+    return fail(ENC_ERR_INVALID, "debug_gelu_table: ready in {-1, 0, 1}, entry in [-1, 65535], value in [-1, 65535]");
+  hipError_t e = enc::gemm_debug_gelu_table(ready, entry, value, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail_hip(e, "debug_gelu_table launch");
+  return ok();
+}
+
 int enc_layernorm_bf16(const void* x, const void* gamma, const void* beta, void* y, int64_t rows,
                        int64_t width, float eps, const uint8_t* row_mask, void* stream) {
   if (rows < 0 || width <= 0) return fail(ENC_ERR_INVALID, "layernorm: rows must be >= 0 and width > 0");

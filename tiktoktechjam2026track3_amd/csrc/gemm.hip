@@ -79,6 +79,16 @@ __global__ void gelu_ready_kernel() {
   __hip_atomic_store(&g_gelu_ready, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Test hooks: set the ready flag, and overwrite (value >= 0) or recompute
+// (value < 0) one table entry.
+__global__ void gelu_flag_set_kernel(uint32_t ready) {
+  __hip_atomic_store(&g_gelu_ready, ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__global__ void gelu_entry_set_kernel(uint32_t x, int32_t value) {
+  g_gelu_table[x] = value < 0 ? f32_to_bf16(gelu_erf(__uint_as_float(x << 16))) : static_cast<uint16_t>(value);
+}
+
 // The wide kernel's GELU epilogue reads a compact copy of the table from LDS:
 // for each sign, the bf16 magnitudes a = bits & 0x7fff in [kGeluLo, kGeluHi]
 // (|x| from 2.4e-4 to 5.53; 7.2 KiB for both signs, which leaves two 256x128
@@ -520,10 +530,15 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
   const int wn = wave & 1;
   const int l32 = lane & 31;
   const int lhi = lane >> 5;
-  // the GELU table's ready flag, read now so that its latency hides behind
-  // the K loop (a plain load: a stale 0 only selects the erf)
+  // The GELU table's ready flag, read by wavefront 0 now (an agent-scope
+  // atomic load, so it sees the value in memory rather than a cached copy)
+  // and handed to the workgroup through LDS at the last K block's barrier:
+  // one verdict per workgroup, taken before any table word is read.  A clear flag
+  // (a product on another stream racing the first fill) selects the erf.
   uint32_t gelu_flag = 0u;
-  if constexpr (EPI == kEpiBiasGelu) gelu_flag = g_gelu_ready;
+  if constexpr (EPI == kEpiBiasGelu) {
+    if (wave == 0) gelu_flag = __hip_atomic_load(&g_gelu_ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 
   // Load instruction j of wavefront w fills LDS rows R (4 j + w) .. + R - 1
   // (R = rows per instruction); lane -> row + lane / chunks, slot lane % chunks,
@@ -677,6 +692,12 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
 #pragma unroll
       for (int j = 0; j < RN; ++j) bf[j] = bn[j];
     }
+    if constexpr (EPI == kEpiBiasGelu) {
+      // last block: every load has to land before this barrier anyway, so
+      // wavefront 0 publishes its flag reading here at no cost, in the slot
+      // after the compact table (outside the ring and the staging area)
+      if (!next && tid == 0) reinterpret_cast<uint32_t*>(smem + T::kSmem)[kGeluSpan] = gelu_flag;
+    }
     wait_vm(next ? later : 0);  // loads requested after block kt + 1; the epilogue reuses the ring
     ring_barrier();
     bf16x8 an[RM], bn[RN];
@@ -734,24 +755,28 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
     for (int p = 0; p < kDepth; ++p) load_residual(p, res[p], keep[p]);
   }
   bf16_t* sc = smem;  // every wave passed the last barrier: the stages are free
-  // GELU: the compact table's words are requested now, so their latency
-  // overlaps the staging below, and written to LDS before the staging
-  // barrier, together with thread 0's reading of the table's ready flag.
-  // After the barrier every wavefront takes that one verdict, so the whole
-  // workgroup either reads the LDS table or evaluates the erf.  (The words
-  // are read and written either way; before the table is filled they are
-  // never used.)
+  // GELU: the workgroup's verdict (wavefront 0's reading of the ready flag,
+  // in LDS since the last K block's barrier).  With the table, its compact words are
+  // requested now, so their latency overlaps the staging below, and written
+  // to LDS before the staging barrier.  No table word is read before a flag
+  // reading of 1, and the flag is set on the fill's stream after the fill
+  // kernel ended (its writes are in memory by then), so no cache can hold a
+  // word from before the fill; with a clear flag the words are never read.
   bf16_t* gelu_tab = smem + T::kSmem;
   constexpr int kGeluWords = kGeluSpan;  // 4-byte words of both slices
   constexpr int kGeluWordsPerThread = (kGeluWords + kThreads - 1) / kThreads;
+  const bool table =
+      EPI == kEpiBiasGelu && __builtin_amdgcn_readfirstlane(reinterpret_cast<const uint32_t*>(gelu_tab)[kGeluWords]) != 0;
   uint32_t gelu_words[EPI == kEpiBiasGelu ? kGeluWordsPerThread : 1];
   if constexpr (EPI == kEpiBiasGelu) {
+    if (table) {
 #pragma unroll
-    for (int i = 0; i < kGeluWordsPerThread; ++i) {
-      const int w = tid + i * kThreads;  // word w of the LDS table
-      const int half_words = kGeluSpan / 2;
-      const uint32_t src = (w < half_words ? kGeluLo : 0x8000u + kGeluLo) + 2u * (w % half_words);
-      if (w < kGeluWords) gelu_words[i] = *reinterpret_cast<const uint32_t*>(&g_gelu_table[src]);
+      for (int i = 0; i < kGeluWordsPerThread; ++i) {
+        const int w = tid + i * kThreads;  // word w of the LDS table
+        const int half_words = kGeluSpan / 2;
+        const uint32_t src = (w < half_words ? kGeluLo : 0x8000u + kGeluLo) + 2u * (w % half_words);
+        if (w < kGeluWords) gelu_words[i] = *reinterpret_cast<const uint32_t*>(&g_gelu_table[src]);
+      }
     }
   }
 #pragma unroll
@@ -775,16 +800,15 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
     for (int p = 0; p < kDepth; ++p) load_residual(p, res[p], keep[p]);
   }
   if constexpr (EPI == kEpiBiasGelu) {
+    if (table) {
 #pragma unroll
-    for (int i = 0; i < kGeluWordsPerThread; ++i) {
-      const int w = tid + i * kThreads;
-      if (w < kGeluWords) reinterpret_cast<uint32_t*>(gelu_tab)[w] = gelu_words[i];
+      for (int i = 0; i < kGeluWordsPerThread; ++i) {
+        const int w = tid + i * kThreads;
+        if (w < kGeluWords) reinterpret_cast<uint32_t*>(gelu_tab)[w] = gelu_words[i];
+      }
     }
-    if (tid == 0) reinterpret_cast<uint32_t*>(gelu_tab)[kGeluWords] = gelu_flag;
   }
   __syncthreads();
-  const bool table =
-      EPI == kEpiBiasGelu && __builtin_amdgcn_readfirstlane(reinterpret_cast<const uint32_t*>(gelu_tab)[kGeluWords]) != 0;
   // Every row of the tile is in range (all tiles but the last tile row): the
   // passes then run without a per-row branch, so the compiler can batch their
   // LDS reads and stores.  Uniform.
@@ -1284,6 +1308,18 @@ hipError_t ensure_gelu_table(hipStream_t st) {
   if (e == hipSuccess && capture == hipStreamCaptureStatusNone) g_gelu_enqueued[dev] = true;
   return e;
 }
+
+}  // namespace
+
+hipError_t gemm_debug_gelu_table(int32_t ready, int32_t entry, int32_t value, hipStream_t st) {
+  hipError_t e = ensure_gelu_table(st);
+  if (e != hipSuccess) return e;
+  if (entry >= 0) hipLaunchKernelGGL(gelu_entry_set_kernel, dim3(1), dim3(1), 0, st, static_cast<uint32_t>(entry), value);
+  if (ready >= 0) hipLaunchKernelGGL(gelu_flag_set_kernel, dim3(1), dim3(1), 0, st, static_cast<uint32_t>(ready));
+  return hipGetLastError();
+}
+
+namespace {
 
 template <int BM, int BN, int BK, int NS, int OCC = 1>
 hipError_t launch_big(const bf16_t* A, const bf16_t* W, int M, int N, int K, int epi,

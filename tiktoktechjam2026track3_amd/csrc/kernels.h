@@ -70,6 +70,11 @@ void gemm_order_clear();
 // Whether gemm_bf16 would accumulate some tile of this product in two partials.
 bool gemm_has_split_tail(int64_t M, int64_t N, int64_t K, int num_cus);
 
+// Test hook for the wide kernel's GELU table: ready >= 0 sets the device's
+// ready flag (0: every GELU epilogue evaluates the erf); entry >= 0
+// overwrites that table entry with value, or recomputes it when value < 0.
+hipError_t gemm_debug_gelu_table(int32_t ready, int32_t entry, int32_t value, hipStream_t stream);
+
 // Tile shape the dispatcher picks for (M, N) on a device with num_cus CUs.
 void gemm_pick_tile(int64_t M, int64_t N, int epilogue, int num_cus, int* bm, int* bn);
 // K-split reduction order matching torch.nn.functional.linear for this shape:

@@ -46,6 +46,7 @@ SIGNATURES = (
     ("enc_last_error", ctypes.c_char_p, ()),
     ("enc_linear_order_register", ctypes.c_int, (_I32, _I64, _I64, _I64, _I32, _I32, _I32, _VP)),
     ("enc_linear_order_clear", ctypes.c_int, ()),
+    ("enc_debug_gelu_table", ctypes.c_int, (_I32, _I32, _I32, _VP)),
     ("enc_layernorm_bf16", ctypes.c_int, (_VP, _VP, _VP, _VP, _I64, _I64, _F32, _VP, _VP)),
     ("enc_linear_bf16", ctypes.c_int, (_VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I32, _VP, _VP)),
     ("enc_prepack_weight_bf16", ctypes.c_int, (_VP, _VP, _I64, _I64, _VP)),
@@ -304,6 +305,12 @@ def ffn(
         ),
     )
     return out
+
+
+def debug_gelu_table(device: torch.device, ready: int = -1, entry: int = -1, value: int = -1) -> None:
+    """Test hook (enc_debug_gelu_table): set the GELU table's ready flag and/or
+    overwrite (value >= 0) or restore (value -1) one table entry."""
+    _check("enc_debug_gelu_table", load_library().enc_debug_gelu_table(ready, entry, value, _stream(device)))
 
 
 def vt_stride(seq_len: int) -> int:
