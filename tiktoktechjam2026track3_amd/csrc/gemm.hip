@@ -594,8 +594,12 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
     for (int j = 0; j < RN; ++j) bf[j] = *reinterpret_cast<const bf16x8*>(st + b_off + j * 32 * BK + slot);
   };
   constexpr int KS = BK / 16;              // 16-wide K steps per block
-  constexpr int kPer = T::kLoads / KS;     // load instructions issued per step
-  static_assert(T::kLoads % KS == 0, "a block's loads split evenly over its steps");
+  // With two stages (NS == 2) block kt + 1's loads must all be requested
+  // before block kt's barrier, so they go out over its first KS - 1 steps;
+  // with more stages they are spread over all KS steps.
+  constexpr int kLoadSteps = NS == 2 ? KS - 1 : KS;
+  constexpr int kPer = (T::kLoads + kLoadSteps - 1) / kLoadSteps;  // load instructions issued per step
+  static_assert(NS == 2 || T::kLoads % KS == 0, "a block's loads split evenly over its steps");
   // Part `part` of a block's loads: instructions [part * kPer, (part + 1) * kPer)
   // of the list (A rows, then W rows).
   // (The global loads are written out here rather than in helper lambdas: a
@@ -605,7 +609,7 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
     bf16_t* sa = smem + stage * T::kStage;
 #pragma unroll
     for (int q = 0; q < T::kLoads; ++q) {
-      if (q < part * kPer || q >= (part + 1) * kPer) continue;
+      if (q < part * kPer || q >= (part + 1) * kPer || q >= T::kLoads) continue;
       const bool is_a = q < T::kLoadsA;
       const int row = T::kRowsPerLoad * (4 * (is_a ? q : q - T::kLoadsA) + wave);
       const uint32_t off =
@@ -621,8 +625,8 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
   // Wait until at most n of this thread's load instructions are in flight and
   // its LDS reads are done (n is one of the counts the K loop uses; anything
   // else waits for everything).
-  constexpr int kSteadyLater = (NS - 2) * T::kLoads - kPer;
-  static_assert(NS >= 3 && NS <= 4 && kSteadyLater >= 0 && 2 * T::kLoads < 64, "vmcnt range");
+  constexpr int kSteadyLater = NS == 2 ? 0 : (NS - 2) * T::kLoads - kPer;
+  static_assert(NS >= 2 && NS <= 4 && kSteadyLater >= 0 && 2 * T::kLoads < 64, "vmcnt range");
   auto wait_vm = [&](int n) {
     if (n == kSteadyLater) {
       __builtin_amdgcn_s_waitcnt(waitcnt_imm(kSteadyLater, 0));
@@ -665,7 +669,7 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
   // K block kt (in LDS stage `stage`).  Every step multiplies while the next
   // step's fragments are read and one part of block kt + NS - 1 is requested
   // into the stage block kt - 1 freed, so the loads are spread over the
-  // block instead of bunched.  Before the last step comes the one barrier:
+  // block instead of bunched (with two stages, over all steps but the last).  Before the last step comes the one barrier:
   // block kt + 1 has landed for every wavefront and nobody reads stage `stage`
   // any more; the last step then reads step 0 of block kt + 1, so no LDS or
   // memory latency is left exposed between blocks.
@@ -701,10 +705,10 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
     wait_vm(next ? later : 0);  // loads requested after block kt + 1; the epilogue reuses the ring
     ring_barrier();
     bf16x8 an[RM], bn[RN];
-    if (load) issue_part(lstage, lk0, KS - 1);
+    if (load && NS > 2) issue_part(lstage, lk0, KS - 1);
     if (next) read_frags(stage + 1 == NS ? 0 : stage + 1, 0, an, bn);
     mfma_step(af, bf);
-    if (load) {
+    if (load && NS > 2) {
       interleave<RM * RN, RM + RN, kPer>();
     } else if (next) {
       interleave<RM * RN, RM + RN, 0>();
@@ -1731,7 +1735,7 @@ hipError_t gemm_bf16_plain(const bf16_t* A, const bf16_t* W, int64_t M, int64_t 
   const bool big_ok = epi != kEpiQkvHeadMajor || ep.head_dim % 8 == 0;
   switch (big_ok ? pick_big_tile(M, N, A, W, ep, ep_overlaps, num_cus) : 0) {
     case 256129: return launch_big<256, 128, 32, 3, 2>(A, W, m, n, k, epi, ep, stream);
-    case 256256: return launch_big<256, 256, 32, 4>(A, W, m, n, k, epi, ep, stream);
+    case 256256: return launch_big<256, 256, 64, 2>(A, W, m, n, k, epi, ep, stream);
     case 256128: return launch_big<256, 128, 64, 3>(A, W, m, n, k, epi, ep, stream);
     case 128128: return launch_big<128, 128, 64, 3>(A, W, m, n, k, epi, ep, stream);
     default: break;
