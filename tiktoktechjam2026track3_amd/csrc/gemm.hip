@@ -1591,8 +1591,10 @@ int pick_big_tile(int64_t M, int64_t N, const bf16_t* A, const bf16_t* W, const 
   // With two resident 256x128 tiles per CU one tile's epilogue overlaps the
   // other's MFMA loop (when there are tiles for two per CU: a narrow N leaves
   // most CUs idle).  It pays where the epilogue is long against the K loop:
-  // the erf GELU (long dependent VALU work), and the residual epilogues at
-  // K <= 1024 (32768x1024x1024: 88 vs 95 us; at K = 4096 it is slower).
+  // the GELU (32768x4096x1024: 314 vs 366 us on 256x256 tiles).  The
+  // residual epilogues run as fast or faster on the 256x256 tiles
+  // (32768x1024x1024 plain weight: 73.5 vs 83.2 us; 409600x1024x1024 packed:
+  // 932 vs 1007 us).
   if (ep_overlaps && N % 128 == 0 && t256x128 >= 2 * num_cus) return 256129;
   // Whole rounds of tiles over the CUs times the tile's work, over its
   // measured per-tile efficiency (256x128 tiles run ~10% below 256x256).
@@ -1728,14 +1730,19 @@ hipError_t gemm_bf16_plain(const bf16_t* A, const bf16_t* W, int64_t M, int64_t 
   if (split == 4 && chunk == 32) return launch_split<4, 32>(A, W, m, n, k, epi, ep, stream);
   if (split == 4 && chunk == 64) return launch_split<4, 64>(A, W, m, n, k, epi, ep, stream);
   if (split == 2 && chunk == 128) return launch_split<2, 128>(A, W, m, n, k, epi, ep, stream);
-  const bool residual = epi == kEpiResidualKeep || epi == kEpiResidualZero;
-  const bool ep_overlaps = epi == kEpiBiasGelu || (residual && K <= 1024);
+  const bool ep_overlaps = epi == kEpiBiasGelu;
   // The large-tile head-major epilogue stores 8 channels of one head at a
   // time (Q, K) and channel pairs (V^T): head_dim must be a multiple of 8.
   const bool big_ok = epi != kEpiQkvHeadMajor || ep.head_dim % 8 == 0;
   switch (big_ok ? pick_big_tile(M, N, A, W, ep, ep_overlaps, num_cus) : 0) {
     case 256129: return launch_big<256, 128, 32, 3, 2>(A, W, m, n, k, epi, ep, stream);
-    case 256256: return launch_big<256, 256, 64, 2>(A, W, m, n, k, epi, ep, stream);
+    // 256x256 tiles: from the plain nn.Linear weight, 64-deep K blocks in two
+    // stages (32768x3072x1024: 190 vs 201 us); from the tile-packed copy,
+    // whose 32-deep slices make each load one 1 KiB run, 32-deep blocks in
+    // four stages (197 vs 225 us).  A/B in one process, bitwise the same.
+    case 256256:
+      if (ep.w_packed != nullptr) return launch_big<256, 256, 32, 4>(A, W, m, n, k, epi, ep, stream);
+      return launch_big<256, 256, 64, 2>(A, W, m, n, k, epi, ep, stream);
     case 256128: return launch_big<256, 128, 64, 3>(A, W, m, n, k, epi, ep, stream);
     case 128128: return launch_big<128, 128, 64, 3>(A, W, m, n, k, epi, ep, stream);
     default: break;

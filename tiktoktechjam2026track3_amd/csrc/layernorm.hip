@@ -86,13 +86,16 @@ layernorm_kernel(const bf16_t* __restrict__ x, const bf16_t* __restrict__ gamma,
   }
   float mean_all, m2_all;
   if constexpr (WIDTH >= 1024) {
-    // Every virtual thread holds the same number of elements, so the four
-    // trees can share registers once half of a tree's lanes are idle: each
-    // merge below pairs the same two virtual lanes, in the same operand
-    // order, as the per-warp tree.
+    // Every virtual thread holds the same number of elements (C0 = WIDTH /
+    // 256), so every merge combines two equal power-of-two counts and takes
+    // welford_merge_equal's constant weights; and the four trees can share
+    // registers once half of a tree's lanes are idle: each merge below pairs
+    // the same two virtual lanes, in the same operand order, as the per-warp
+    // tree.
+    constexpr int C0 = WIDTH / 256;
     // Level 32 per virtual warp: lanes 0..31 of each hold its live states.
 #pragma unroll
-    for (int w = 0; w < 4; ++w) st[w] = welford_merge(st[w], shfl_down(st[w], 32));
+    for (int w = 0; w < 4; ++w) st[w] = welford_merge_equal<C0>(st[w], shfl_down_stats(st[w], 32));
     // Pack: p01 = warp 0 in lanes 0..31, warp 1 in lanes 32..63; p23 likewise.
     const bool upper32 = lane >= 32;
     Welford p01 = st[0], p23 = st[2];
@@ -107,8 +110,8 @@ layernorm_kernel(const bf16_t* __restrict__ x, const bf16_t* __restrict__ gamma,
       }
     }
     // Level 16 within each 32-lane half.
-    p01 = welford_merge(p01, shfl_down(p01, 16));
-    p23 = welford_merge(p23, shfl_down(p23, 16));
+    p01 = welford_merge_equal<2 * C0>(p01, shfl_down_stats(p01, 16));
+    p23 = welford_merge_equal<2 * C0>(p23, shfl_down_stats(p23, 16));
     // Pack: q = warp 0 | warp 2 | warp 1 | warp 3 in lanes 0..15 | 16..31 |
     // 32..47 | 48..63 (lanes with bit 4 set take p23 from lane ^ 16).
     Welford q = p01;
@@ -121,11 +124,13 @@ layernorm_kernel(const bf16_t* __restrict__ x, const bf16_t* __restrict__ gamma,
     }
     // Levels 8..1 within each 16-lane group: lanes 0, 16, 32, 48 end with the
     // totals of warps 0, 2, 1, 3.
-#pragma unroll
-    for (int off = 8; off > 0; off >>= 1) q = welford_merge(q, shfl_down(q, off));
+    q = welford_merge_equal<4 * C0>(q, shfl_down_stats(q, 8));
+    q = welford_merge_equal<8 * C0>(q, shfl_down_stats(q, 4));
+    q = welford_merge_equal<16 * C0>(q, shfl_down_stats(q, 2));
+    q = welford_merge_equal<32 * C0>(q, shfl_down_stats(q, 1));
     // Cross-warp merges: (0 <- 2) at lane 0, (1 <- 3) at lane 32, then (0 <- 1).
-    q = welford_merge(q, shfl_down(q, 16));
-    q = welford_merge(q, shfl_down(q, 32));
+    q = welford_merge_equal<64 * C0>(q, shfl_down_stats(q, 16));
+    q = welford_merge_equal<128 * C0>(q, shfl_down_stats(q, 32));
     mean_all = q.mean;
     m2_all = q.m2;
   } else {

@@ -43,6 +43,27 @@ __device__ __forceinline__ Welford welford_merge(Welford b, Welford a) {
   return {mean, m2, n};
 }
 
+// welford_merge of two states that both hold C elements, C a power of two
+// (every merge of a row whose virtual threads all hold the same count): the
+// weights a.count * rcp(2C) and b.count * rcp(2C) are exactly 0.5 (v_rcp_f32
+// of a power of two is exact), so they are constants, and the same rounded
+// operations remain: mean = 0.5 a.mean + 0.5 b.mean, m2 = fma(delta^2 C,
+// 0.5, a.m2 + b.m2).
+template <int C>
+__device__ __forceinline__ Welford welford_merge_equal(Welford b, Welford a) {
+#pragma clang fp contract(off)
+  static_assert(C > 0 && (C & (C - 1)) == 0, "equal power-of-two counts");
+  const float delta = b.mean - a.mean;
+  const float mean = 0.5f * a.mean + 0.5f * b.mean;
+  const float m2 = fmaf(delta * delta * static_cast<float>(C), 0.5f, a.m2 + b.m2);
+  return {mean, m2, static_cast<float>(2 * C)};
+}
+
+// mean and m2 only: the count is known to both sides
+__device__ __forceinline__ Welford shfl_down_stats(Welford s, int off) {
+  return {__shfl_down(s.mean, off, kWave), __shfl_down(s.m2, off, kWave), s.count};
+}
+
 __device__ __forceinline__ Welford shfl_down(Welford s, int off) {
   return {__shfl_down(s.mean, off, kWave), __shfl_down(s.m2, off, kWave),
           __shfl_down(s.count, off, kWave)};
