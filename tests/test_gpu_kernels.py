@@ -574,6 +574,20 @@ def test_attention_config_shapes_bitwise(device, b, h, s, causal, prefix):
         assert torch.equal(ref, out)
 
 
+@pytest.mark.parametrize("b,h,s,q_gain", [(16, 16, 300, 1.0), (8, 16, 777, 1.0), (8, 16, 1024, 12.0)])
+def test_attention_causal_half_tile_rows_bitwise(device, b, h, s, q_gain):
+    """Causal unmasked rows of 257-1024 keys with enough rows to fill the
+    chip take the three-wavefront kernel that runs sweeps B and C one 32-key
+    half tile at a time; a ragged last tile (300, 777) and scores large
+    enough for weights below 2^-100 (q_gain 12: the IEEE division path) must
+    still give the oracle's bits."""
+    q, k, v, v_t = _attention_inputs(device, b, h, s, 5 * s + b)
+    q = (q.float() * q_gain).bfloat16()
+    out = native.attention(q, k, v_t, 0.125, True)
+    ref = _oracle_context(q, k, v, True, None)
+    assert torch.equal(ref, out), f"max abs {_context_error(ref, out)}"
+
+
 @pytest.mark.parametrize(
     "hd,b,h,s,causal,prefix,exact",
     [
