@@ -574,18 +574,34 @@ def test_attention_config_shapes_bitwise(device, b, h, s, causal, prefix):
         assert torch.equal(ref, out)
 
 
-@pytest.mark.parametrize("b,h,s,q_gain", [(16, 16, 300, 1.0), (8, 16, 777, 1.0), (8, 16, 1024, 12.0)])
-def test_attention_causal_half_tile_rows_bitwise(device, b, h, s, q_gain):
-    """Causal unmasked rows of 257-1024 keys with enough rows to fill the
-    chip take the three-wavefront kernel that runs sweeps B and C one 32-key
-    half tile at a time; a ragged last tile (300, 777) and scores large
-    enough for weights below 2^-100 (q_gain 12: the IEEE division path) must
-    still give the oracle's bits."""
+@pytest.mark.parametrize(
+    "b,h,s,causal,prefix,q_gain",
+    [(16, 16, 300, True, False, 1.0), (8, 16, 777, True, False, 1.0), (8, 16, 1024, True, False, 12.0),
+     (4, 16, 2048, True, False, 1.0), (8, 16, 1000, False, False, 1.0), (8, 16, 1024, False, True, 1.0)],
+)
+def test_attention_half_tile_rows_bitwise(device, b, h, s, causal, prefix, q_gain):
+    """Head-dim-64 rows of 257-2048 keys with enough rows to fill the chip
+    (causal without key masks; non-causal past 512 keys, with or without a
+    prefix mask) take the three-wavefront kernel that runs sweeps B and C one
+    32-key half tile at a time.  A ragged last tile (300, 777, 1000), padded
+    keys, and scores large enough for weights below 2^-100 (q_gain 12: the
+    IEEE division path) must still give the oracle's bits."""
     q, k, v, v_t = _attention_inputs(device, b, h, s, 5 * s + b)
     q = (q.float() * q_gain).bfloat16()
-    out = native.attention(q, k, v_t, 0.125, True)
-    ref = _oracle_context(q, k, v, True, None)
-    assert torch.equal(ref, out), f"max abs {_context_error(ref, out)}"
+    kv_len = mask = None
+    if prefix:
+        g = torch.Generator(device=device).manual_seed(s + 7)
+        lengths = torch.randint(s // 2, s + 1, (b,), generator=g, device=device)
+        mask = torch.arange(s, device=device)[None, :] < lengths[:, None]
+        kv_len = lengths.int()
+    out = native.attention(q, k, v_t, 0.125, causal, kv_len=kv_len)
+    ref = _oracle_context(q, k, v, causal, mask)
+    if mask is not None:
+        valid = mask[..., None].expand_as(out)
+        assert torch.equal(ref[valid], out[valid]), f"max abs {_context_error(ref[valid], out[valid])}"
+        assert torch.all(out[~valid] == 0)
+    else:
+        assert torch.equal(ref, out), f"max abs {_context_error(ref, out)}"
 
 
 @pytest.mark.parametrize(

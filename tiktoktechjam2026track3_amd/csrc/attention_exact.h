@@ -122,9 +122,9 @@ __device__ __forceinline__ int tile_key(int kb32, int r, int h) {
 // both tiles, with wavefront 1's probabilities.
 // OCC is the wavefronts per SIMD the register allocation must allow (1: no
 // bound).  Long head-dim-64 rows with at least four workgroups per CU use 4
-// (at most 128 VGPRs, a few spilled; see dispatch_order); causal unmasked
-// head-dim-64 rows of at most 1024 keys use 3 with the half-tile sweeps
-// (kHalfTiles: at most 168 VGPRs).
+// (at most 128 VGPRs, a few spilled; see dispatch_order); most head-dim-64
+// short rows use 3 with the half-tile sweeps (kHalfTiles: at most 168
+// VGPRs, see dispatch_order).
 template <int HD, int NW, bool CAUSAL, int MASK, bool POW2_SCALE, bool BLOCK_ORDER, int RES, int OCC>
 __global__ void __launch_bounds__(NW * kWave, OCC)
 attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
@@ -139,9 +139,9 @@ attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
   constexpr bool kFoldScale = POW2_SCALE && !BLOCK_ORDER;
   // Short rows streamed through the ring at three wavefronts per SIMD: sweeps
   // B and C work on one 32-key half of a tile at a time, so that half of the
-  // scores, weights and P fragments are live at once (178 instead of 250
-  // VGPRs; 168 with 3 spilled at the bound).  Same MFMA chains and per-score
-  // operations in the same order, so the same bits.
+  // scores, weights and P fragments are live at once (at most 168 VGPRs
+  // instead of 250, none spilled).  Same MFMA chains and per-score operations
+  // in the same order, so the same bits.
   constexpr bool kHalfTiles = !BLOCK_ORDER && RES == 0 && OCC == 3;
   constexpr int kThreads = NW * kWave;
   constexpr int kBQ = kSplit ? 32 : NW * 32;
@@ -605,16 +605,21 @@ attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
     }
   };
   // sweep B on one half: its 16 weights added to their partials
+  // (The weights replace the gaps in place under the branch and are added
+  // after it: with the adds inside the two paths, both halves' partials were
+  // copied between registers at the join, 32 moves per half.)
   auto sum_half = [&](int buf, int k0, int kb32, bool masked, bool clamp, float (&p)[16]) __attribute__((always_inline)) {
     f32x16 sh;
     gaps_half(buf, k0, kb32, masked, sh);
     if (clamp) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) p[r] += exp_gap(sh[r]);
+      for (int r = 0; r < 16; ++r) sh[r] = exp_gap(sh[r]);
     } else {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) p[r] += exp_gap_unclamped(sh[r]);
+      for (int r = 0; r < 16; ++r) sh[r] = exp_gap_unclamped(sh[r]);
     }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) p[r] += sh[r];
   };
 
   // ======================= sweep B: row sum of exp(s - max) =======================
@@ -849,9 +854,16 @@ attn_fwd_kernel(const bf16_t* __restrict__ Q, const bf16_t* __restrict__ Kg,
 #pragma unroll
       for (int r = 0; r < 16; ++r) pf2[r >> 3][r & 7] = static_cast<__bf16>(exp_gap(sh[r]) / row_sum);
     } else {
+      if (masked) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sh[r] = exp_gap(sh[r]);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sh[r] = exp_gap_unclamped(sh[r]);
+      }
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float e = masked ? exp_gap(sh[r]) : exp_gap_unclamped(sh[r]);
+        const float e = sh[r];
         const float q = e * inv_sum;
         const float p = fmaf(fmaf(-q, row_sum, e), inv_sum, q);
         pf2[r >> 3][r & 7] = static_cast<__bf16>(p);
@@ -1023,14 +1035,17 @@ hipError_t dispatch_order(const bf16_t* q, const bf16_t* k, const bf16_t* vt, bf
     if (S <= 4 * kBKV)
       return launch_attn<HD, 4, CAUSAL, MASK, POW2, false, 4>(q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
   }
-  // Causal, unmasked, head dim 64, rows of at most 1024 keys: three
-  // wavefronts per SIMD with the half-tile sweeps (H = 16: B = 8, S = 1024
-  // 102.1 -> 95.3 us; S = 777 75.1 -> 69.8; B = 16, S = 300 38.6 -> 31.3).
-  // The two-wavefront kernel stays faster without the causal mask (S = 512
-  // 41.2 vs 43.4 us), with key masks (prefix, S = 1000: 71.3 vs 83.3) and
-  // past 1024 keys (S = 2048 154.7 vs 155.2).
-  if constexpr (HD == 64 && CAUSAL && MASK == 0) {
-    if (S <= 1024)
+  // Head dim 64: three wavefronts per SIMD with the half-tile sweeps where
+  // they measured faster (H = 16, one process, bitwise the same): causal
+  // without key masks (B = 8: S = 1024 103.9 -> 93.2 us, S = 777 72.6 ->
+  // 63.6; B = 16, S = 300 38.7 -> 30.3; B = 4, S = 2048 153.8 -> 148.1) and
+  // non-causal rows of more than 512 keys with or without a prefix mask
+  // (B = 8, S = 1024: 144.1 -> 137.9, prefix 134.5 -> 128.5).  The
+  // two-wavefront kernel stays for causal prefix masks (S = 1000: 68.6 vs
+  // 77.3), byte masks (S = 900: 138.9 vs 144.6) and non-causal rows of up to
+  // 512 keys (40.9 vs 42.0).
+  if constexpr (HD == 64 && MASK != kMaskBytes && !(CAUSAL && MASK == kMaskPrefix)) {
+    if (CAUSAL || S > 512)
       return launch_attn<HD, 4, CAUSAL, MASK, POW2, false, 0, 3>(q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
   }
   return launch_attn<HD, 4, CAUSAL, MASK, POW2, false>(q, k, vt, ctx, B, H, S, scale, kv_len, key_mask, st);
