@@ -211,3 +211,15 @@ def test_failing_pass_reports_its_output(tmp_path, monkeypatch):
     argv = ["--encoder-configs", "c2", "--profile-candidate", "--rocprof", "--rocprof-dir", str(tmp_path / "p")]
     with pytest.raises(RuntimeError, match="status 3:\n.*no device here"):
         runner.collect_rocprof(runner.parse_args(argv), argv)
+
+
+def test_short_names_keep_anonymous_namespace_kernels():
+    from tiktoktechjam2026track3_amd.profiling import short_name
+
+    assert short_name("void enc::(anonymous namespace)::gemm_big_kernel<256, 256, 32, 4, 4, 1>(unsigned short const*, int)") \
+        == "gemm_big_kernel<256, 256, 32, 4, 4, 1>"
+    assert short_name("void (anonymous namespace)::softmax_warp_forward<float, float, float, 7, false, false>(float*, int)") \
+        == "softmax_warp_forward<float, float, float, 7, false, false>"
+    assert short_name("void at::native::(anonymous namespace)::distribution_kernel<float, 4>(long, float*)") \
+        == "at::native::distribution_kernel<float, 4>"
+    assert short_name("__amd_rocclr_copyBuffer") == "__amd_rocclr_copyBuffer"

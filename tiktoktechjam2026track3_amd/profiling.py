@@ -434,7 +434,8 @@ def _find(directory: str, suffix: str) -> str:
 def short_name(name: str, limit: int = 72) -> str:
     """Kernel name without namespaces and argument list, template kept,
     cut to ``limit`` characters."""
-    name = name.replace("void ", "").replace("enc::(anonymous namespace)::", "")
+    name = name.replace("void ", "").replace("(anonymous namespace)::", "")
+    name = name.replace("enc::", "", 1) if name.startswith("enc::") else name
     depth = 0
     for i, ch in enumerate(name):
         if ch == "<":
