@@ -575,17 +575,21 @@ def test_attention_config_shapes_bitwise(device, b, h, s, causal, prefix):
 
 
 @pytest.mark.parametrize(
-    "b,h,s,causal,prefix,q_gain",
-    [(16, 16, 300, True, False, 1.0), (8, 16, 777, True, False, 1.0), (8, 16, 1024, True, False, 12.0),
-     (4, 16, 2048, True, False, 1.0), (8, 16, 1000, False, False, 1.0), (8, 16, 1024, False, True, 1.0)],
+    "b,h,s,causal,prefix,q_gain,scale",
+    [(16, 16, 300, True, False, 1.0, 0.125), (8, 16, 777, True, False, 1.0, 0.125),
+     (8, 16, 1024, True, False, 12.0, 0.125), (4, 16, 2048, True, False, 1.0, 0.125),
+     (8, 16, 1000, False, False, 1.0, 0.125), (8, 16, 1024, False, True, 1.0, 0.125),
+     (8, 16, 1024, True, False, 1.0, 0.1), (8, 16, 1000, False, True, 4.0, 0.1)],
 )
-def test_attention_half_tile_rows_bitwise(device, b, h, s, causal, prefix, q_gain):
+def test_attention_half_tile_rows_bitwise(device, b, h, s, causal, prefix, q_gain, scale):
     """Head-dim-64 rows of 257-2048 keys with enough rows to fill the chip
     (causal without key masks; non-causal past 512 keys, with or without a
     prefix mask) take the three-wavefront kernel that runs sweeps B and C one
     32-key half tile at a time.  A ragged last tile (300, 777, 1000), padded
-    keys, and scores large enough for weights below 2^-100 (q_gain 12: the
-    IEEE division path) must still give the oracle's bits."""
+    keys, scores large enough for weights below 2^-100 (q_gain 12: the IEEE
+    division path) and a scale that is not a power of two (0.1: the scores
+    rounded twice, bf16(bf16(q.k) * scale)) must still give the oracle's
+    bits."""
     q, k, v, v_t = _attention_inputs(device, b, h, s, 5 * s + b)
     q = (q.float() * q_gain).bfloat16()
     kv_len = mask = None
@@ -594,8 +598,9 @@ def test_attention_half_tile_rows_bitwise(device, b, h, s, causal, prefix, q_gai
         lengths = torch.randint(s // 2, s + 1, (b,), generator=g, device=device)
         mask = torch.arange(s, device=device)[None, :] < lengths[:, None]
         kv_len = lengths.int()
-    out = native.attention(q, k, v_t, 0.125, causal, kv_len=kv_len)
-    ref = _oracle_context(q, k, v, causal, mask)
+    out = native.attention(q, k, v_t, scale, causal, kv_len=kv_len)
+    ctx = attention_rows(q, k, v, scale, causal, mask, torch.arange(s, device=device))
+    ref = ctx.transpose(1, 2).reshape(b, s, h * 64)
     if mask is not None:
         valid = mask[..., None].expand_as(out)
         assert torch.equal(ref[valid], out[valid]), f"max abs {_context_error(ref[valid], out[valid])}"
