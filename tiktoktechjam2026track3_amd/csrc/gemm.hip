@@ -574,12 +574,14 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
     for (int j = 0; j < RN; ++j) bf[j] = *reinterpret_cast<const bf16x8*>(st + b_off + j * 32 * BK + slot);
   };
   constexpr int KS = BK / 16;              // 16-wide K steps per block
-  // With two stages (NS == 2) block kt + 1's loads must all be requested
-  // before block kt's barrier, so they go out over its first KS - 1 steps;
-  // with more stages they are spread over all KS steps.
-  constexpr int kLoadSteps = NS == 2 ? KS - 1 : KS;
-  constexpr int kPer = (T::kLoads + kLoadSteps - 1) / kLoadSteps;  // load instructions issued per step
-  static_assert(NS == 2 || T::kLoads % KS == 0, "a block's loads split evenly over its steps");
+  // A block's loads go out in KS parts, one per step.  With more than two
+  // stages, block kt + NS - 1's parts go out over block kt's steps.  With two
+  // stages (NS == 2) block kt + 1's loads must all be requested before block
+  // kt's barrier, so its part 0 goes out in block kt - 1's last step (after
+  // that block's barrier, when the stage it read is free) and parts 1 .. KS-1
+  // over block kt's first KS - 1 steps.
+  constexpr int kPer = T::kLoads / KS;  // load instructions issued per step
+  static_assert(T::kLoads % KS == 0, "a block's loads split evenly over its steps");
   // Part `part` of a block's loads: instructions [part * kPer, (part + 1) * kPer)
   // of the list (A rows, then W rows).
   // (The global loads are written out here rather than in helper lambdas: a
@@ -614,6 +616,8 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
       __builtin_amdgcn_s_waitcnt(waitcnt_imm(T::kLoads, 0));
     } else if (n == 2 * T::kLoads) {
       __builtin_amdgcn_s_waitcnt(waitcnt_imm(2 * T::kLoads, 0));
+    } else if (n == kPer) {
+      __builtin_amdgcn_s_waitcnt(waitcnt_imm(kPer, 0));
     } else {
       __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
     }
@@ -670,34 +674,44 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
     }
   };
 
-  // Prologue: blocks 0 .. NS-2 in full; block NS-1 loads during block 0.
+  // Prologue: blocks 0 .. NS-2 in full; block NS-1 loads during block 0
+  // (two stages: block 1's part 0 goes out here, after block 0's loads).
   const int KT = K / BK;
   const int prologue = min(NS - 1, KT);
   for (int p = 0; p < prologue; ++p)
 #pragma unroll
     for (int part = 0; part < KS; ++part) issue_part(p, p * BK, part);
-  wait_vm((prologue - 1) * T::kLoads);
+  if (NS == 2 && KT > 1) {
+    issue_part(1, BK, 0);
+    wait_vm(kPer);
+  } else {
+    wait_vm((prologue - 1) * T::kLoads);
+  }
   ring_barrier();
   bf16x8 af[RM], bf[RN];
   read_frags(0, 0, af, bf);
 
   // K block kt (in LDS stage `stage`).  Every step multiplies while the next
-  // step's fragments are read and one part of block kt + NS - 1 is requested
-  // into the stage block kt - 1 freed, so the loads are spread over the
-  // block instead of bunched (with two stages, over all steps but the last).  Before the last step comes the one barrier:
+  // step's fragments are read and one part of a later block's loads is
+  // requested into a free stage, so the loads are spread over the block
+  // instead of bunched.  Before the last step comes the one barrier:
   // block kt + 1 has landed for every wavefront and nobody reads stage `stage`
   // any more; the last step then reads step 0 of block kt + 1, so no LDS or
-  // memory latency is left exposed between blocks.
+  // memory latency is left exposed between blocks.  `load` covers the parts
+  // issued before the barrier, `load_last` the last step's part (two stages:
+  // part 0 of block kt + 2, into stage `stage`).
   // (A plain lambda called with constant flags: a generic lambda makes clang
   // drop the kernel's host-side launch stub, and runtime flags would merge
   // differently scheduled MFMA results and double the accumulator registers.)
-  auto k_block = [&](int kt, int stage, int later, bool load, bool next) __attribute__((always_inline)) {
+  auto k_block = [&](int kt, int stage, int later, bool load, bool next, bool load_last)
+      __attribute__((always_inline)) {
     const int lstage = stage == 0 ? NS - 1 : stage - 1;  // stage of block kt + NS - 1
     const int lk0 = (kt + NS - 1) * BK;
+    constexpr int kPart0 = NS == 2 ? 1 : 0;  // part of the first step
 #pragma unroll
     for (int ks = 0; ks + 1 < KS; ++ks) {
       bf16x8 an[RM], bn[RN];
-      step_explicit(af, bf, an, bn, stage, ks + 1, true, lstage, lk0, ks, load);
+      step_explicit(af, bf, an, bn, stage, ks + 1, true, lstage, lk0, ks + kPart0, load);
 #pragma unroll
       for (int i = 0; i < RM; ++i) af[i] = an[i];
 #pragma unroll
@@ -712,7 +726,10 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
     wait_vm(next ? later : 0);  // loads requested after block kt + 1; the epilogue reuses the ring
     ring_barrier();
     bf16x8 an[RM], bn[RN];
-    step_explicit(af, bf, an, bn, stage + 1 == NS ? 0 : stage + 1, 0, next, lstage, lk0, KS - 1, load && NS > 2);
+    if constexpr (NS == 2)
+      step_explicit(af, bf, an, bn, stage + 1 == NS ? 0 : stage + 1, 0, next, stage, lk0 + BK, 0, load_last);
+    else
+      step_explicit(af, bf, an, bn, stage + 1 == NS ? 0 : stage + 1, 0, next, lstage, lk0, KS - 1, load_last);
     if (next) {
 #pragma unroll
       for (int i = 0; i < RM; ++i) af[i] = an[i];
@@ -722,15 +739,28 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
   };
   int stage = 0;
   int kt = 0;
-  for (; kt + NS - 1 < KT; ++kt) {
-    k_block(kt, stage, kSteadyLater, true, true);
-    stage = stage + 1 == NS ? 0 : stage + 1;
+  if constexpr (NS == 2) {
+    // every load in flight at a block's barrier is for the next block
+    for (; kt + 2 < KT; ++kt) {
+      k_block(kt, stage, 0, true, true, true);
+      stage ^= 1;
+    }
+    if (kt + 1 < KT) {
+      k_block(kt, stage, 0, true, true, false);
+      stage ^= 1;
+      ++kt;
+    }
+  } else {
+    for (; kt + NS - 1 < KT; ++kt) {
+      k_block(kt, stage, kSteadyLater, true, true, true);
+      stage = stage + 1 == NS ? 0 : stage + 1;
+    }
+    for (; kt + 1 < KT; ++kt) {
+      k_block(kt, stage, (KT - 2 - kt) * T::kLoads, false, true, false);
+      stage = stage + 1 == NS ? 0 : stage + 1;
+    }
   }
-  for (; kt + 1 < KT; ++kt) {
-    k_block(kt, stage, (KT - 2 - kt) * T::kLoads, false, true);
-    stage = stage + 1 == NS ? 0 : stage + 1;
-  }
-  k_block(kt, stage, 0, false, false);
+  k_block(kt, stage, 0, false, false, false);
 
   // ---- epilogue: y = bf16(acc + bias) into LDS, then 8 outputs per thread ----
   constexpr int kPerRow = BN / 8;
