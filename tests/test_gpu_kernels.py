@@ -444,6 +444,7 @@ def test_qkv_head_major(device, b, s, d, h):
     assert within_ulps(ref[2].transpose(-1, -2), v_t[..., :s], 1)
     packed = F.linear(x, w, bias).view(b, s, 3, h, hd).permute(2, 0, 3, 1, 4)
     assert bitwise_fraction(packed[0], q) > 0.999 and bitwise_fraction(packed[1], k) > 0.999
+    assert bitwise_fraction(packed[2].transpose(-1, -2), v_t[..., :s]) > 0.999
 
 
 def test_softmax_exp_matches_device_expf_exhaustively(device):
