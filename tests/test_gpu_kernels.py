@@ -354,9 +354,10 @@ def test_prepack_weight_layout(device, n, k):
         (1100, 128, 1024, native.ENC_EPI_BIAS),                # 128x128x64 tiles
         (100000, 1024, 1024, native.ENC_EPI_BIAS),             # stream-K tail rows read the plain weight
         (200, 1024, 1024, native.ENC_EPI_BIAS),                # few rows: the packed copy goes unread
-        # 256x256x32 tiles in the four-stage ring: the shortest K (four
-        # blocks), a few blocks, and K % 128 == 64, each with a ragged last
-        # tile row
+        # 256x256 tiles: one and two 64-deep blocks in the two-stage ring
+        # (plain weight), two to 130 32-deep blocks in the four-stage ring
+        # (packed), K % 128 == 64, each with a ragged last tile row
+        (8292, 1024, 64, native.ENC_EPI_BIAS_RESIDUAL_ZERO),
         (8292, 1024, 128, native.ENC_EPI_BIAS_RESIDUAL_KEEP),
         (4100, 2048, 320, native.ENC_EPI_BIAS_RESIDUAL_ZERO),
         (8292, 1024, 4160, native.ENC_EPI_BIAS_RESIDUAL_KEEP),
