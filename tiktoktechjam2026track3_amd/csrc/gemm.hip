@@ -552,28 +552,50 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
   const i32x4 w_rsrc = buffer_rsrc(w_tile);
   const int w_row0 = w_packed ? n0 % pn : 0;
 
-  f32x16 acc[RM][RN];
+  // kM16 (the four-stage ring of 32-deep blocks): v_mfma_f32_16x16x32_bf16
+  // on 16x16 blocks, one MFMA per block and K block; otherwise
+  // v_mfma_f32_32x32x16_bf16 on 32x32 blocks, two 16-deep steps per 32 of K.
+  // Each output is the same chain of 16-term dot products either way
+  // (bitwise the same); the 16x16x32 form moves half the accumulator
+  // registers per product, and under the power cap its launches run at a
+  // higher shader clock.
+  constexpr bool kM16 = BK == 32 && NS == 4 && BM == 256 && BN == 256 && EPI != kEpiBiasGelu;
+  constexpr int FM = kM16 ? BM / 32 : RM;  // fragments per wavefront along M (16 or 32 rows each)
+  constexpr int FN = kM16 ? BN / 32 : RN;  // ... along N
+  constexpr int kFR = kM16 ? 16 : 32;      // rows per fragment
+  f32x16 acc[kM16 ? 1 : RM][kM16 ? 1 : RN];
+  f32x4 acc4[kM16 ? FM : 1][kM16 ? FN : 1];
+  if constexpr (kM16) {
 #pragma unroll
-  for (int i = 0; i < RM; ++i)
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < RN; ++j)
+      for (int j = 0; j < FN; ++j) acc4[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  } else {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+    for (int i = 0; i < RM; ++i)
+#pragma unroll
+      for (int j = 0; j < RN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  }
 
-  // Fragment rows: A row wm*(BM/2) + 32 i + l32, W row wn*(BN/2) + 32 j + l32;
-  // the row's low bits are l32's, so the swizzle is per lane.
-  const int a_off = (wm * (BM / 2) + l32) * BK;
-  const int b_off = BM * BK + (wn * (BN / 2) + l32) * BK;
-  const int swz = T::swz(l32);
-  auto read_frags = [&](int stage, int ks, bf16x8 (&af)[RM], bf16x8 (&bf)[RN]) {
+  // Fragment rows: A row wm*(BM/2) + kFR i + fr, W row wn*(BN/2) + kFR j + fr
+  // (fr = the lane's row in the fragment); the row's low bits are fr's, so the
+  // swizzle is per lane.  A lane reads 8 consecutive k: chunk fk of the step.
+  const int fr = kM16 ? lane % 16 : l32;
+  const int fk = kM16 ? lane / 16 : lhi;
+  const int a_off = (wm * (BM / 2) + fr) * BK;
+  const int b_off = BM * BK + (wn * (BN / 2) + fr) * BK;
+  const int swz = T::swz(fr);
+  auto read_frags = [&](int stage, int ks, bf16x8 (&af)[FM], bf16x8 (&bf)[FN]) {
     const bf16_t* st = smem + stage * T::kStage;
-    const int slot = ((2 * ks + lhi) ^ swz) * 8;
+    const int slot = ((kM16 ? fk : 2 * ks + fk) ^ swz) * 8;
 #pragma unroll
-    for (int i = 0; i < RM; ++i) af[i] = *reinterpret_cast<const bf16x8*>(st + a_off + i * 32 * BK + slot);
+    for (int i = 0; i < FM; ++i) af[i] = *reinterpret_cast<const bf16x8*>(st + a_off + i * kFR * BK + slot);
 #pragma unroll
-    for (int j = 0; j < RN; ++j) bf[j] = *reinterpret_cast<const bf16x8*>(st + b_off + j * 32 * BK + slot);
+    for (int j = 0; j < FN; ++j) bf[j] = *reinterpret_cast<const bf16x8*>(st + b_off + j * kFR * BK + slot);
   };
-  constexpr int KS = BK / 16;              // 16-wide K steps per block
+  constexpr int KS = kM16 ? 1 : BK / 16;  // MFMA steps per block
   // A block's loads go out in KS parts, one per step.  With more than two
   // stages, block kt + NS - 1's parts go out over block kt's steps.  With two
   // stages (NS == 2) block kt + 1's loads must all be requested before block
@@ -640,7 +662,7 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
   // and seven reads between two MFMAs, which the one wavefront per SIMD
   // issues in order while its MFMA pipe idles: the fixed order is 2-5%
   // faster on the wide products, bitwise the same.
-  auto step_explicit = [&](const bf16x8 (&a)[RM], const bf16x8 (&b)[RN], bf16x8 (&an)[RM], bf16x8 (&bn)[RN],
+  auto step_explicit = [&](const bf16x8 (&a)[FM], const bf16x8 (&b)[FN], bf16x8 (&an)[FM], bf16x8 (&bn)[FN],
                            int rstage, int rks, bool read, int lstage, int lk0, int part, bool load)
       __attribute__((always_inline)) {
     const bf16_t* rs = smem + rstage * T::kStage;
@@ -649,7 +671,7 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
 #pragma unroll
     for (int q = 0; q < RM * RN; ++q) {
       const int i = q / RN, j = q % RN;
-      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b[j], a[i], acc[i][j], 0, 0, 0);
+      if constexpr (!kM16) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b[j], a[i], acc[i][j], 0, 0, 0);
       if (read && q < RM) an[q] = *reinterpret_cast<const bf16x8*>(rs + a_off + q * 32 * BK + slot);
       if (read && q >= RM && q < RM + RN)
         bn[q - RM] = *reinterpret_cast<const bf16x8*>(rs + b_off + (q - RM) * 32 * BK + slot);
@@ -677,10 +699,12 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
   // Prologue: blocks 0 .. NS-2 in full; block NS-1 loads during block 0
   // (two stages: block 1's part 0 goes out here, after block 0's loads).
   const int KT = K / BK;
-  const int prologue = min(NS - 1, KT);
+  // (kM16: always NS - 1 blocks, past the last block re-reading it into a
+  // stage nobody reads, so that every block's wait is the same)
+  const int prologue = kM16 ? NS - 1 : min(NS - 1, KT);
   for (int p = 0; p < prologue; ++p)
 #pragma unroll
-    for (int part = 0; part < KS; ++part) issue_part(p, p * BK, part);
+    for (int part = 0; part < KS; ++part) issue_part(p, min(p, KT - 1) * BK, part);
   if (NS == 2 && KT > 1) {
     issue_part(1, BK, 0);
     wait_vm(kPer);
@@ -688,8 +712,20 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
     wait_vm((prologue - 1) * T::kLoads);
   }
   ring_barrier();
-  bf16x8 af[RM], bf[RN];
-  read_frags(0, 0, af, bf);
+  bf16x8 af[FM], bf[FN];
+  if constexpr (kM16) {
+    // block 0's W fragments 0..3, then its A fragments: the order in which
+    // each block reads the next one's, so that the compiler's LDS waits at
+    // the top of the K loop are the same from the loop's entry and its back
+    // edge (W fragments 4..7 are read inside the block)
+    const int slot = (fk ^ swz) * 8;
+#pragma unroll
+    for (int j = 0; j < FN / 2; ++j) bf[j] = *reinterpret_cast<const bf16x8*>(smem + b_off + j * kFR * BK + slot);
+#pragma unroll
+    for (int i = 0; i < FM; ++i) af[i] = *reinterpret_cast<const bf16x8*>(smem + a_off + i * kFR * BK + slot);
+  } else {
+    read_frags(0, 0, af, bf);
+  }
 
   // K block kt (in LDS stage `stage`).  Every step multiplies while the next
   // step's fragments are read and one part of a later block's loads is
@@ -710,7 +746,7 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
     constexpr int kPart0 = NS == 2 ? 1 : 0;  // part of the first step
 #pragma unroll
     for (int ks = 0; ks + 1 < KS; ++ks) {
-      bf16x8 an[RM], bn[RN];
+      bf16x8 an[FM], bn[FN];
       step_explicit(af, bf, an, bn, stage, ks + 1, true, lstage, lk0, ks + kPart0, load);
 #pragma unroll
       for (int i = 0; i < RM; ++i) af[i] = an[i];
@@ -725,7 +761,7 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
     }
     wait_vm(next ? later : 0);  // loads requested after block kt + 1; the epilogue reuses the ring
     ring_barrier();
-    bf16x8 an[RM], bn[RN];
+    bf16x8 an[FM], bn[FN];
     if constexpr (NS == 2)
       step_explicit(af, bf, an, bn, stage + 1 == NS ? 0 : stage + 1, 0, next, stage, lk0 + BK, 0, load_last);
     else
@@ -739,7 +775,63 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
   };
   int stage = 0;
   int kt = 0;
-  if constexpr (NS == 2) {
+  if constexpr (kM16) {
+    // One 32-deep block, one step: after the wait for block kt + 1 and the
+    // barrier, its 64 MFMAs in two halves (W fragments j = 0..3, then 4..7,
+    // A fragments i-major inside each).  The fragments are read in place,
+    // each after its last use, so there is one register set and no copies:
+    // this block's W fragments 4..7 over the first half; the next block's W
+    // fragments 0..3 (last used in the first half) and A fragment i (after
+    // its last MFMA) over the second.  Loads go out one per eight MFMAs, for
+    // block kt + 3 (clamped to the last block).
+    auto step16 = [&](int cstage, int nstage, bool next, int lstage, int lk0, bool load)
+        __attribute__((always_inline)) {
+      const bf16_t* cs = smem + cstage * T::kStage;
+      const bf16_t* ns = smem + nstage * T::kStage;
+      const int slot = (fk ^ swz) * 8;
+      bf16_t* sa = smem + lstage * T::kStage;
+#pragma unroll
+      for (int q = 0; q < FM * FN; ++q) {
+        const int h = q / (FM * FN / 2), i = (q % (FM * FN / 2)) / (FN / 2), j = (FN / 2) * h + q % (FN / 2);
+        acc4[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf[j], af[i], acc4[i][j], 0, 0, 0);
+        if (q < FN / 2)
+          bf[FN / 2 + q] = *reinterpret_cast<const bf16x8*>(cs + b_off + (FN / 2 + q) * kFR * BK + slot);
+        if (next && h == 1 && q - FM * FN / 2 < FN / 2)
+          bf[q - FM * FN / 2] = *reinterpret_cast<const bf16x8*>(ns + b_off + (q - FM * FN / 2) * kFR * BK + slot);
+        if (next && h == 1 && q % (FN / 2) == FN / 2 - 1)
+          af[i] = *reinterpret_cast<const bf16x8*>(ns + a_off + i * kFR * BK + slot);
+        constexpr int kLS = (FM * FN) / kPer;
+        if (load && q % kLS == kLS / 2) {
+          const int lq = q / kLS;
+          const bool is_a = lq < T::kLoadsA;
+          const int row = T::kRowsPerLoad * (4 * (is_a ? lq : lq - T::kLoadsA) + wave);
+          const uint32_t off =
+              is_a ? static_cast<uint32_t>(min(row + lrow, a_rows_left) * K + gcol) * 2u
+              : w_packed ? static_cast<uint32_t>((gcol >> 5) * pn * 32 + (w_row0 + row + lrow) * 32 + (gcol & 31)) * 2u
+                         : static_cast<uint32_t>((row + lrow) * K + gcol) * 2u;
+          enc_buffer_load_lds(is_a ? a_rsrc : w_rsrc,
+                              reinterpret_cast<__attribute__((address_space(3))) uint32_t*>(
+                                  reinterpret_cast<uintptr_t>(sa + (is_a ? 0 : BM * BK) + row * BK)),
+                              16, static_cast<int>(off), is_a ? 2 * lk0 : 2 * lk0 * w_k_mul, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+    for (; kt + 1 < KT; ++kt) {
+      const int nstage = stage + 1 == NS ? 0 : stage + 1;
+      // block kt + 1 has landed; block kt + 2's loads may be in flight, and so
+      // may the read of block kt + 1's last A fragment (its stage is not
+      // written before block kt + 2's barrier)
+      __builtin_amdgcn_s_waitcnt(waitcnt_imm(kSteadyLater, 15));
+      ring_barrier();
+      step16(stage, nstage, true, stage == 0 ? NS - 1 : stage - 1, min(kt + NS - 1, KT - 1) * BK, true);
+      stage = nstage;
+    }
+    wait_vm(0);
+    ring_barrier();
+    step16(stage, stage, false, stage, 0, false);
+    ring_barrier();  // this block's last fragment reads are done before the epilogue reuses the ring
+  } else if constexpr (NS == 2) {
     // every load in flight at a block's barrier is for the next block
     for (; kt + 2 < KT; ++kt) {
       k_block(kt, stage, 0, true, true, true);
@@ -760,7 +852,7 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
       stage = stage + 1 == NS ? 0 : stage + 1;
     }
   }
-  k_block(kt, stage, 0, false, false, false);
+  if constexpr (!kM16) k_block(kt, stage, 0, false, false, false);
 
   // ---- epilogue: y = bf16(acc + bias) into LDS, then 8 outputs per thread ----
   constexpr int kPerRow = BN / 8;
@@ -812,19 +904,36 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
       }
     }
   }
+  if constexpr (kM16) {
+    // 16x16 blocks: lane l holds row (token) l % 16 and the four consecutive
+    // columns 4 (l / 16) .. + 3 of block (i, j)
 #pragma unroll
-  for (int j = 0; j < RN; ++j) {
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int cl = wn * (BN / 2) + j * 32 + 8 * g + 4 * lhi;  // four consecutive columns
+    for (int j = 0; j < FN; ++j) {
+      const int cl = wn * (BN / 2) + j * 16 + 4 * fk;  // four consecutive columns
       const u32x2 bb = *reinterpret_cast<const u32x2*>(ep.bias + n0 + cl);
       const float b0 = lo_bf16(bb[0]), b1 = hi_bf16(bb[0]), b2 = lo_bf16(bb[1]), b3 = hi_bf16(bb[1]);
 #pragma unroll
-      for (int i = 0; i < RM; ++i) {
-        const int rl = wm * (BM / 2) + i * 32 + l32;
+      for (int i = 0; i < FM; ++i) {
+        const int rl = wm * (BM / 2) + i * 16 + fr;
         *reinterpret_cast<u32x2*>(sc + rl * T::kLdc + cl) =
-            u32x2{pack_bf16x2(acc[i][j][4 * g] + b0, acc[i][j][4 * g + 1] + b1),
-                  pack_bf16x2(acc[i][j][4 * g + 2] + b2, acc[i][j][4 * g + 3] + b3)};
+            u32x2{pack_bf16x2(acc4[i][j][0] + b0, acc4[i][j][1] + b1), pack_bf16x2(acc4[i][j][2] + b2, acc4[i][j][3] + b3)};
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < RN; ++j) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int cl = wn * (BN / 2) + j * 32 + 8 * g + 4 * lhi;  // four consecutive columns
+        const u32x2 bb = *reinterpret_cast<const u32x2*>(ep.bias + n0 + cl);
+        const float b0 = lo_bf16(bb[0]), b1 = hi_bf16(bb[0]), b2 = lo_bf16(bb[1]), b3 = hi_bf16(bb[1]);
+#pragma unroll
+        for (int i = 0; i < RM; ++i) {
+          const int rl = wm * (BM / 2) + i * 32 + l32;
+          *reinterpret_cast<u32x2*>(sc + rl * T::kLdc + cl) =
+              u32x2{pack_bf16x2(acc[i][j][4 * g] + b0, acc[i][j][4 * g + 1] + b1),
+                    pack_bf16x2(acc[i][j][4 * g + 2] + b2, acc[i][j][4 * g + 3] + b3)};
+        }
       }
     }
   }
