@@ -85,7 +85,7 @@ def test_layernorm_matches_torch(device, rows, width):
     assert torch.equal(torch_bf16, out)
 
 
-@pytest.mark.parametrize("width", [32, 128, 512, 1024, 4096])
+@pytest.mark.parametrize("width", [32, 128, 256, 512, 1024, 4096])
 def test_layernorm_merge_order_rows(device, width):
     """Rows holding one large value and two values just under half an ulp of
     it: whether the two small ones survive depends on which partial

@@ -134,18 +134,35 @@ layernorm_kernel(const bf16_t* __restrict__ x, const bf16_t* __restrict__ gamma,
     mean_all = q.mean;
     m2_all = q.m2;
   } else {
-    // shuffle-down trees of the four virtual warps (lane 0 holds each result)
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-#pragma unroll
-      for (int w = 0; w < 4; ++w) st[w] = welford_merge(st[w], shfl_down(st[w], off));
+    // WIDTH 256 or 512: virtual threads 0 .. WIDTH/4 - 1 (virtual warps 0 and,
+    // at 512, 1) hold one 4-element vector each and the others none.  Inside
+    // a non-empty warp every merge combines two equal power-of-two counts
+    // (welford_merge_equal); an empty warp's tree stays empty; and merging an
+    // empty state into a state of 256 elements is an identity (weights
+    // 0 * rcp(256) = 0 and 256 * rcp(256) = 1, both exact), so of the
+    // cross-warp merges only (0 <- 1) at 512 changes anything.
+    static_assert(WIDTH == 256 || WIDTH == 512, "one vector per virtual thread of warps 0 (and 1)");
+    const bool upper32 = lane >= 32;
+    st[0] = welford_merge_equal<4>(st[0], shfl_down_stats(st[0], 32));
+    Welford q = st[0];
+    if constexpr (WIDTH == 512) {
+      // warp 1's level 32, then warp 0 in lanes 0..31 and warp 1 in 32..63
+      st[1] = welford_merge_equal<4>(st[1], shfl_down_stats(st[1], 32));
+      const float m1 = __shfl_xor(st[1].mean, 32, kWave), q1 = __shfl_xor(st[1].m2, 32, kWave);
+      if (upper32) {
+        q.mean = m1;
+        q.m2 = q1;
+      }
     }
-    // cross-warp merges: (0 <- 2), (1 <- 3), then (0 <- 1)
-    Welford w0 = welford_merge(st[0], st[2]);
-    const Welford w1 = welford_merge(st[1], st[3]);
-    w0 = welford_merge(w0, w1);
-    mean_all = w0.mean;
-    m2_all = w0.m2;
+    // levels 16..1 within each 32-lane half (lane 0: warp 0, lane 32: warp 1)
+    q = welford_merge_equal<8>(q, shfl_down_stats(q, 16));
+    q = welford_merge_equal<16>(q, shfl_down_stats(q, 8));
+    q = welford_merge_equal<32>(q, shfl_down_stats(q, 4));
+    q = welford_merge_equal<64>(q, shfl_down_stats(q, 2));
+    q = welford_merge_equal<128>(q, shfl_down_stats(q, 1));
+    if constexpr (WIDTH == 512) q = welford_merge_equal<256>(q, shfl_down_stats(q, 32));
+    mean_all = q.mean;
+    m2_all = q.m2;
   }
   const float mean = __shfl(mean_all, 0, kWave);
   const float var = __shfl(m2_all, 0, kWave) / static_cast<float>(WIDTH);
