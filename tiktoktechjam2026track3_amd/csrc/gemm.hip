@@ -868,11 +868,17 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
   // are never stored.
   constexpr int kDepth = kPasses < 2048 / BN ? kPasses : 2048 / BN;  // 16 or 8: within the register budget
   u32x4 res[kResidual ? kDepth : 1];
-  bool keep[kResidual ? kDepth : 1];
-  auto load_residual = [&](int p, u32x4& r, bool& k) {
+  // The mask bytes are held untested until their pass: a test here would
+  // wait for the byte's load, and with it for every load requested before
+  // it.  Without a mask the loads read the residual's first byte (any valid
+  // address), which the pass ignores.
+  uint32_t keep[kResidual ? kDepth : 1];
+  const bool has_mask = ep.row_mask != nullptr;
+  const uint8_t* mask_bytes = has_mask ? ep.row_mask : reinterpret_cast<const uint8_t*>(ep.residual);
+  auto load_residual = [&](int p, u32x4& r, uint32_t& k) {
     const int row = min(m0 + rl0 + p * kRowsPerPass, M - 1);
     r = *reinterpret_cast<const u32x4*>(ep.residual + static_cast<int64_t>(row) * N + n0 + c8);
-    k = ep.row_mask == nullptr || ep.row_mask[row] != 0;
+    k = mask_bytes[has_mask ? row : 0];
   };
   // (256-wide tiles: requested after the staging, which needs the registers)
   if constexpr (kResidual && BN <= 128) {
@@ -967,7 +973,7 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
         if (all_rows || row < M) {
           const u32x4 v = *reinterpret_cast<const u32x4*>(sc + rl * T::kLdc + c8);
           if constexpr (kResidual) {
-            finish8<EPI>(ep, N, row, n0 + c8, v, res[p % kDepth], keep[p % kDepth]);
+            finish8<EPI>(ep, N, row, n0 + c8, v, res[p % kDepth], !has_mask || keep[p % kDepth] != 0u);
           } else {
             finish8<EPI>(ep, N, row, n0 + c8, v, u32x4{0u, 0u, 0u, 0u}, true, gelu_table, gelu_tab);
           }
