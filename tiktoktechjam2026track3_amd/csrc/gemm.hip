@@ -555,10 +555,10 @@ gemm_big_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int 
   // kM16 (the four-stage ring of 32-deep blocks): v_mfma_f32_16x16x32_bf16
   // on 16x16 blocks, one MFMA per block and K block; otherwise
   // v_mfma_f32_32x32x16_bf16 on 32x32 blocks, two 16-deep steps per 32 of K.
-  // Each output is the same chain of 16-term dot products either way
-  // (bitwise the same); the 16x16x32 form moves half the accumulator
-  // registers per product, and under the power cap its launches run at a
-  // higher shader clock.
+  // On MI355X the two forms give bitwise the same outputs (both match
+  // torch's products on every tested shape); the 16x16x32 form moves half
+  // the accumulator registers per product, and under the power cap its
+  // launches run at a higher shader clock.
   constexpr bool kM16 = BK == 32 && NS == 4 && BM == 256 && BN == 256 && EPI != kEpiBiasGelu;
   constexpr int FM = kM16 ? BM / 32 : RM;  // fragments per wavefront along M (16 or 32 rows each)
   constexpr int FN = kM16 ? BN / 32 : RN;  // ... along N
