@@ -361,6 +361,10 @@ def test_prepack_weight_layout(device, n, k):
         (8292, 1024, 128, native.ENC_EPI_BIAS_RESIDUAL_KEEP),
         (4100, 2048, 320, native.ENC_EPI_BIAS_RESIDUAL_ZERO),
         (8292, 1024, 4160, native.ENC_EPI_BIAS_RESIDUAL_KEEP),
+        # c4's out_proj and ffn_out shapes with a row mask (the residual
+        # epilogue's prefetched mask bytes)
+        (32768, 1024, 1024, native.ENC_EPI_BIAS_RESIDUAL_KEEP),
+        (32768, 1024, 4096, native.ENC_EPI_BIAS_RESIDUAL_ZERO),
     ],
 )
 def test_linear_prepacked_is_bitwise_the_plain_product(device, m, n, k, epi):
@@ -379,6 +383,14 @@ def test_linear_prepacked_is_bitwise_the_plain_product(device, m, n, k, epi):
     assert mismatches == 0
     if epi == native.ENC_EPI_BIAS:
         assert torch.equal(packed, F.linear(a, w, bias))
+    elif residual is not None:
+        # masked rows: the residual (keep) or zero, the others torch's sum
+        ref = residual + F.linear(a, w, bias)
+        assert bitwise_fraction(ref[mask], packed[mask]) > 0.999
+        if epi == native.ENC_EPI_BIAS_RESIDUAL_KEEP:
+            assert torch.equal(packed[~mask], residual[~mask])
+        else:
+            assert torch.all(packed[~mask] == 0)
 
 
 def test_linear_prepacked_rejects_unpackable_shapes(device):
