@@ -1187,7 +1187,9 @@ __device__ __forceinline__ void store_one(const GemmEpilogueArgs& ep, int N, int
   }
 }
 
-template <int EPI, int SPLIT, int CW, int KS>
+// R: LDS stages in the ring, all requested ahead (R - 1 in flight while one
+// is multiplied)
+template <int EPI, int SPLIT, int CW, int KS, int R = 2>
 __global__ void __launch_bounds__(256)
 gemm_skinny_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, int M, int N, int K,
                    GemmEpilogueArgs ep) {
@@ -1202,7 +1204,9 @@ gemm_skinny_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, i
   static_assert(KS == 128 || KS == 256, "stage width");
   static_assert(kRows % (kRowsPerLoad * kWaves) == 0, "load split");
   static_assert(SPLIT == 1 || (CW % 16 == 0 && KS % (CW * SPLIT) == 0), "chunk width");
-  __shared__ __attribute__((aligned(16))) bf16_t smem[2 * kStage];
+  static_assert(R >= 2 && (R & (R - 1)) == 0 && (R - 1) * kLoads < 64, "ring depth");
+  static_assert(R * kStage * 2 + SPLIT * 64 * 4 * 4 <= 160 * 1024, "LDS budget");
+  __shared__ __attribute__((aligned(16))) bf16_t smem[R * kStage];
   __shared__ float red[SPLIT > 1 ? SPLIT : 1][64][4];
 
   const int tiles_m = (M + 15) / 16;
@@ -1283,13 +1287,20 @@ gemm_skinny_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, i
   }
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   const int nst = K / KS;
-  issue_stage(0, 0);
-  if (nst > 1) issue_stage(1, KS);
+  if constexpr (R == 2) {
+    issue_stage(0, 0);
+    if (nst > 1) issue_stage(1, KS);
+  } else {
+#pragma unroll
+    for (int st = 0; st < R; ++st)
+      if (st < nst) issue_stage(st, st * KS);
+  }
   for (int st = 0; st < nst; ++st) {
-    const int buf = st & 1;
-    // the other stage's loads may still be in flight
-    if (st + 1 < nst) {
-      __builtin_amdgcn_s_waitcnt(waitcnt_imm(kLoads, 0));
+    const int buf = st & (R - 1);
+    // the next R - 1 stages' loads may still be in flight (near the end,
+    // fewer are left: wait for all)
+    if (st + R - 1 < nst) {
+      __builtin_amdgcn_s_waitcnt(waitcnt_imm((R - 1) * kLoads, 0));
     } else {
       __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
     }
@@ -1302,7 +1313,7 @@ gemm_skinny_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, i
     }
     __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 0));
     ring_barrier();  // every wavefront is done reading this stage
-    if (st + 2 < nst) issue_stage(buf, (st + 2) * KS);
+    if (st + R < nst) issue_stage(buf, (st + R) * KS);
   }
 
   if constexpr (SPLIT > 1) {
@@ -1336,18 +1347,24 @@ gemm_skinny_kernel(const bf16_t* __restrict__ A, const bf16_t* __restrict__ W, i
   }
 }
 
-template <int SPLIT, int CW, int KS>
+template <int SPLIT, int CW, int KS, int R = 2>
 hipError_t launch_skinny(const bf16_t* A, const bf16_t* W, int M, int N, int K, int epi,
                          const GemmEpilogueArgs& ep, hipStream_t st) {
+  // K-split tiles (16 KiB stages) over more than two stages of K: four
+  // stages, three in flight (c2's 128x512x2048 ffn_out 6.8 -> 6.15 us per
+  // launch; eight stages gained less)
+  if constexpr (SPLIT > 1 && R == 2) {
+    if (K / KS > 2) return launch_skinny<SPLIT, CW, KS, 4>(A, W, M, N, K, epi, ep, st);
+  }
   constexpr int kWaves = SPLIT == 1 ? 4 : SPLIT;
   constexpr int kBN = SPLIT == 1 ? 64 : 16;
   const dim3 grid(((M + 15) / 16) * (N / kBN)), block(kWaves * kWave);
   switch (epi) {
-    case kEpiBias: hipLaunchKernelGGL((gemm_skinny_kernel<kEpiBias, SPLIT, CW, KS>), grid, block, 0, st, A, W, M, N, K, ep); break;
-    case kEpiBiasGelu: hipLaunchKernelGGL((gemm_skinny_kernel<kEpiBiasGelu, SPLIT, CW, KS>), grid, block, 0, st, A, W, M, N, K, ep); break;
-    case kEpiResidualKeep: hipLaunchKernelGGL((gemm_skinny_kernel<kEpiResidualKeep, SPLIT, CW, KS>), grid, block, 0, st, A, W, M, N, K, ep); break;
-    case kEpiResidualZero: hipLaunchKernelGGL((gemm_skinny_kernel<kEpiResidualZero, SPLIT, CW, KS>), grid, block, 0, st, A, W, M, N, K, ep); break;
-    case kEpiQkvHeadMajor: hipLaunchKernelGGL((gemm_skinny_kernel<kEpiQkvHeadMajor, SPLIT, CW, KS>), grid, block, 0, st, A, W, M, N, K, ep); break;
+    case kEpiBias: hipLaunchKernelGGL((gemm_skinny_kernel<kEpiBias, SPLIT, CW, KS, R>), grid, block, 0, st, A, W, M, N, K, ep); break;
+    case kEpiBiasGelu: hipLaunchKernelGGL((gemm_skinny_kernel<kEpiBiasGelu, SPLIT, CW, KS, R>), grid, block, 0, st, A, W, M, N, K, ep); break;
+    case kEpiResidualKeep: hipLaunchKernelGGL((gemm_skinny_kernel<kEpiResidualKeep, SPLIT, CW, KS, R>), grid, block, 0, st, A, W, M, N, K, ep); break;
+    case kEpiResidualZero: hipLaunchKernelGGL((gemm_skinny_kernel<kEpiResidualZero, SPLIT, CW, KS, R>), grid, block, 0, st, A, W, M, N, K, ep); break;
+    case kEpiQkvHeadMajor: hipLaunchKernelGGL((gemm_skinny_kernel<kEpiQkvHeadMajor, SPLIT, CW, KS, R>), grid, block, 0, st, A, W, M, N, K, ep); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
